@@ -1,0 +1,149 @@
+/*
+ * trntensor_hip.h — C ABI of libtrntensor_hip.so, the gfx950 (MI355X) kernel
+ * library behind trntensor_amd's fused-contraction path.
+ *
+ * The reference (trntensor 0.4.0) has no native code; its device boundary is
+ * the Python module trntensor/nki/dispatch.py, which hands padded, contiguous
+ * tensors to four NKI kernels in trntensor/nki/_kernels.py. Each entry point
+ * below replaces one of those kernels plus its dispatcher; the citation on
+ * each declaration names the reference code it stands in for.
+ *
+ * Conventions (all entry points):
+ *  - Plain pointers and sizes only. Every pointer named "device" is device
+ *    memory on the current HIP device; the library never allocates or frees
+ *    memory and keeps no mutable global state, so calls are re-entrant.
+ *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *    Work is enqueued on it and the call returns without synchronising.
+ *  - dtype codes: TT_F32 = 0 (float), TT_F64 = 1 (double).
+ *  - Return codes: TT_OK 0; TT_INVALID 1 (bad argument: the Python layer
+ *    raises ValueError); TT_UNSUPPORTED 2 (dtype/shape the kernels do not
+ *    cover: NotImplementedError); TT_HIP_ERROR 3 (launch failure:
+ *    RuntimeError). tt_last_error() returns a message for the calling
+ *    thread's last failure.
+ */
+#ifndef TRNTENSOR_HIP_H
+#define TRNTENSOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TT_ABI_VERSION 1
+#define TT_MAX_DIMS 8
+
+enum { TT_OK = 0, TT_INVALID = 1, TT_UNSUPPORTED = 2, TT_HIP_ERROR = 3 };
+enum { TT_F32 = 0, TT_F64 = 1 };
+
+/* ABI version of the loaded library (TT_ABI_VERSION at build time). */
+int tt_abi_version(void);
+
+/* Static name of a status code. */
+const char* tt_status_string(int status);
+
+/* Message for the calling thread's last non-OK return. */
+const char* tt_last_error(void);
+
+/*
+ * Batched strided GEMM on the MFMA core, row-major:
+ *   op(A)[m,k] = transA ? A[k*lda + m] : A[m*lda + k]
+ *   op(B)[k,n] = transB ? B[n*ldb + k] : B[k*ldb + n]
+ *   D[m*ldd + n] = alpha * sum_k op(A)[m,k] op(B)[k,n]  (+ beta * C[m*ldc + n])
+ * for every batch b, each operand offset by b*stride. C is read iff it is
+ * non-NULL (so beta*C is added whenever C is given, like torch's
+ * add(out, alpha=beta)). D may alias C exactly. K may be 0.
+ *
+ * Replaces matmul_kernel (trntensor/nki/_kernels.py:35-75) behind
+ * nki_matmul (trntensor/nki/dispatch.py:187-237) and batched_matmul_kernel
+ * (_kernels.py:77-117) behind nki_batched_matmul (dispatch.py:339-387), and
+ * additionally folds einsum's alpha/beta epilogue (trntensor/einsum.py:99-102)
+ * into the store. No padding: edge tiles are masked in the kernel.
+ */
+int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
+            double alpha, const void* A, int64_t lda, int64_t strideA,
+            const void* B, int64_t ldb, int64_t strideB,
+            double beta, const void* C, int64_t ldc, int64_t strideC,
+            void* D, int64_t ldd, int64_t strideD, int64_t batch, void* stream);
+
+/*
+ * Workspace (device bytes) that tt_mp2_energy needs for this problem.
+ */
+size_t tt_mp2_energy_workspace_bytes(int dtype, int64_t nocc, int64_t nvir, int64_t naux);
+
+/*
+ * Density-fitted MP2 correlation energy
+ *   E = sum_{ijab} T_ijab (2 T_ijab - T_ijba) / (e_i + e_j - e_a - e_b),
+ *   T_ijab = sum_P B[i,a,P] B[j,b,P]
+ * with B contiguous (nocc, nvir, naux), eps_occ (nocc), eps_vir (nvir), all
+ * of `dtype`. Writes one element of `dtype` to energy_out (device). T never
+ * reaches memory: each workgroup forms a 64x64 block of T_ij and its
+ * exchange partner on MFMA, applies the denominator and exchange term in
+ * registers and reduces to one double. deterministic != 0 writes one partial
+ * per workgroup and sums them in a fixed order in a second kernel;
+ * deterministic == 0 adds each workgroup's value with one atomic.
+ *
+ * Replaces mp2_energy_kernel (trntensor/nki/_kernels.py:119-207) behind
+ * _nki_mp2_energy (trntensor/nki/dispatch.py:240-283), without its
+ * nvir <= 128 / naux <= 128 limits (trntensor/quantum.py:72-76).
+ */
+int tt_mp2_energy(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
+                  const void* B, const void* eps_occ, const void* eps_vir,
+                  void* energy_out, void* workspace, size_t workspace_bytes,
+                  int deterministic, void* stream);
+
+/*
+ * Workspace (device bytes) that tt_ao_to_mo_transform needs.
+ */
+size_t tt_ao_to_mo_workspace_bytes(int dtype, int64_t nbasis, int64_t nocc, int64_t nvir, int64_t naux);
+
+/*
+ * Full AO->MO transform B[i,a,P] = sum_{mu,nu} C_occ[mu,i] C_vir[nu,a] eri[mu,nu,P]
+ * with eri contiguous (nbasis, nbasis, naux), C_occ (nbasis, nocc),
+ * C_vir (nbasis, nvir), B_out contiguous (nocc, nvir, naux). Two MFMA GEMMs:
+ * X[i,(nu,P)] = C_occ^T eri viewed (nbasis, nbasis*naux) into the workspace,
+ * then B[i] = C_vir^T X[i] batched over i. All loads are P-contiguous.
+ *
+ * Replaces ao_to_mo_transform_kernel (trntensor/nki/_kernels.py:209-296)
+ * behind _nki_ao_to_mo_transform (trntensor/nki/dispatch.py:286-336),
+ * without its nbasis/nocc/nvir limits (trntensor/quantum.py:161-177).
+ */
+int tt_ao_to_mo_transform(int dtype, int64_t nbasis, int64_t nocc, int64_t nvir, int64_t naux,
+                          const void* eri, const void* C_occ, const void* C_vir,
+                          void* B_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace (device bytes) that tt_strided_contract needs for these extents.
+ */
+size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, const int64_t* out_shape,
+                                           int n_red, const int64_t* red_shape);
+
+/*
+ * Strided multiply-reduce for contractions that have no GEMM shape (outer
+ * products, traces, dots, permutations, letters summed away):
+ *   D[o] = alpha * sum_r A[a_off(o) + a_roff(r)] * B[b_off(o) + b_roff(r)]  (+ beta * C[o])
+ * o runs over out_shape (n_out <= 8 dims, row-major), r over red_shape
+ * (n_red <= 8 dims); offsets are dot products of the multi-index with the
+ * given element strides (0 broadcasts). B may be NULL (single operand:
+ * the factor is 1). D and C are contiguous in out_shape order; C is read iff
+ * non-NULL. Accumulation is in `dtype`.
+ *
+ * No counterpart kernel in the reference: these contractions are the
+ * "torch" strategy, which the reference hands to torch.einsum
+ * (trntensor/einsum.py:117-118) and its path executor's steps
+ * (trntensor/einsum.py:188).
+ */
+int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape,
+                        const int64_t* a_out_strides, const int64_t* b_out_strides,
+                        int n_red, const int64_t* red_shape,
+                        const int64_t* a_red_strides, const int64_t* b_red_strides,
+                        const void* A, const void* B, double alpha, double beta,
+                        const void* C, void* D, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRNTENSOR_HIP_H */

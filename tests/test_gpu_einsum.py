@@ -1,0 +1,263 @@
+"""GPU parity of trntensor_amd.einsum / multi_einsum against the CPU oracle.
+
+The first classes port the reference's own einsum tests
+(tests/test_einsum.py:10-342) onto the HIP path: same inputs, same
+assertions, with the oracle (oracle/cpu_ref.py, the reference's CPU path
+restated) as the expected value and normwise bars of 1e-12 (float64) /
+1e-5 (float32). The config classes run BASELINE.json's shapes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import trntensor_amd as trntensor
+from oracle import brute, cpu_ref
+from tests.util import normwise, rel
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, ref, dt=None):
+    dt = dt or ref.dtype
+    bar = 1e-12 if dt == torch.float64 else 1e-5
+    assert got.dtype == ref.dtype, (got.dtype, ref.dtype)
+    assert tuple(got.shape) == tuple(ref.shape)
+    assert normwise(got, ref) <= bar
+
+
+class TestEinsumReferenceCases:
+    """tests/test_einsum.py:10-84 on the HIP path (CPU operands staged through the GPU)."""
+
+    @pytest.mark.parametrize(
+        "sub,shapes",
+        [
+            ("ij,jk->ik", [(4, 3), (3, 5)]),
+            ("ji,jk->ik", [(3, 4), (3, 5)]),
+            ("ij,kj->ik", [(4, 3), (5, 3)]),
+            ("ji,kj->ik", [(3, 4), (5, 3)]),
+            ("i,i->", [(10,), (10,)]),
+            ("i,j->ij", [(3,), (4,)]),
+            ("ii->", [(5, 5)]),
+            ("bij,bjk->bik", [(8, 4, 3), (8, 3, 5)]),
+            ("ap,bp->ab", [(5, 10), (5, 10)]),
+            ("mi,mnP->inP", [(6, 2), (6, 6, 8)]),
+            ("ijk,jkl->il", [(3, 4, 5), (4, 5, 6)]),
+            ("ij,jk->ik", [(4, 1), (1, 5)]),
+            ("ij,jk,kl->il", [(5, 8), (8, 6), (6, 4)]),
+            ("ij,jk,kl,lm->im", [(3, 5), (5, 4), (4, 6), (6, 2)]),
+            ("ij,ik,il->jkl", [(4, 3), (4, 5), (4, 2)]),
+        ],
+    )
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_matches_oracle(self, hip, sub, shapes, dt):
+        g = torch.Generator().manual_seed(len(sub))
+        ops = [torch.randn(*s, generator=g, dtype=dt) for s in shapes]
+        got = trntensor.einsum(sub, *ops)
+        assert got.device.type == "cpu"
+        close(got, cpu_ref.einsum(sub, *ops))
+
+    def test_device_operands_stay_on_device(self, hip):
+        A, B = torch.randn(64, 48, device="cuda"), torch.randn(48, 80, device="cuda")
+        out = trntensor.einsum("ij,jk->ik", A, B)
+        assert out.device.type == "cuda"
+        close(out.cpu(), cpu_ref.einsum("ij,jk->ik", A.cpu(), B.cpu()))
+
+
+class TestMisplannedPatterns:
+    """Index orders the reference's matmul/bmm executors mishandle
+    (trntensor/plan.py:284-305): the product computes the einsum itself."""
+
+    @pytest.mark.parametrize(
+        "sub,shapes",
+        [
+            ("ij,jk->ki", [(30, 20), (20, 40)]),
+            ("ij,jk->i", [(30, 20), (20, 40)]),
+            ("bji,bjk->bik", [(3, 20, 30), (3, 20, 40)]),
+            ("iap,ibp->iab", [(3, 20, 30), (3, 25, 30)]),
+            ("ibj,bjk->bik", [(20, 3, 30), (3, 30, 40)]),
+        ],
+    )
+    def test_einsum_semantics(self, hip, sub, shapes):
+        g = torch.Generator().manual_seed(7)
+        ops = [torch.randn(*s, generator=g, dtype=torch.float64) for s in shapes]
+        assert cpu_ref.misplanned_by_reference(sub, *ops)
+        got = trntensor.einsum(sub, *ops)
+        ref = torch.from_numpy(np.asarray(brute.einsum_f64(sub, *[o.numpy() for o in ops])))
+        close(got, ref)
+
+
+class TestMultiEinsum:
+    """tests/test_einsum.py:87-150."""
+
+    def test_multiple_and_shared(self, hip):
+        g = torch.Generator().manual_seed(1)
+        A, B, C = (torch.randn(*s, generator=g) for s in [(4, 3), (3, 5), (5, 2)])
+        r = trntensor.multi_einsum(("ij,jk->ik", A, B), ("ij,jk->ik", B, C), ("ij,jk,kl->il", A, B, C), ("ij,ij->", A, A))
+        assert len(r) == 4 and all(x.device.type == "cpu" for x in r)
+        close(r[0], A @ B)
+        close(r[1], B @ C)
+        close(r[2], cpu_ref.einsum("ij,jk,kl->il", A, B, C))
+        close(r[3], cpu_ref.einsum("ij,ij->", A, A))
+
+    def test_shared_operand_views(self, hip):
+        g = torch.Generator().manual_seed(2)
+        Bt = torch.randn(3, 5, 8, generator=g)
+        r = trntensor.multi_einsum(("ap,bp->ab", Bt[0], Bt[1]), ("ap,bp->ab", Bt[1], Bt[0]))
+        close(r[0], cpu_ref.einsum("ap,bp->ab", Bt[0], Bt[1]))
+        close(r[1], cpu_ref.einsum("ap,bp->ab", Bt[1], Bt[0]))
+
+
+class TestAlphaBetaDtypePrecision:
+    """tests/test_einsum.py:216-342."""
+
+    @pytest.mark.parametrize("alpha,beta", [(2.0, 0.0), (1.0, 0.5), (2.0, 0.5), (1.5, 0.5)])
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_alpha_beta(self, hip, alpha, beta, dt):
+        g = torch.Generator().manual_seed(3)
+        A, B, C = (torch.randn(*s, generator=g, dtype=dt) for s in [(40, 30), (30, 50), (40, 50)])
+        got = trntensor.einsum("ij,jk->ik", A, B, alpha=alpha, beta=beta, out=C)
+        close(got, cpu_ref.einsum("ij,jk->ik", A, B, alpha=alpha, beta=beta, out=C))
+        assert torch.equal(C, C.clone())  # out is read, not written
+
+    def test_alpha_beta_through_permute_and_path(self, hip):
+        g = torch.Generator().manual_seed(4)
+        A, B, C = (torch.randn(*s, generator=g, dtype=torch.float64) for s in [(20, 30), (30, 40), (40, 20)])
+        close(trntensor.einsum("ij,jk->ki", A, B, alpha=1.5, beta=0.5, out=C), 1.5 * (A @ B).T + 0.5 * C)
+        D = torch.randn(40, 7, generator=g, dtype=torch.float64)
+        O = torch.randn(20, 7, generator=g, dtype=torch.float64)
+        close(trntensor.einsum("ij,jk,kl->il", A, B, D, alpha=-2.0, beta=3.0, out=O), -2.0 * (A @ B @ D) + 3.0 * O)
+
+    @pytest.mark.parametrize("name,dt", [("bf16", torch.bfloat16), ("fp16", torch.float16), ("f64", torch.float64)])
+    def test_dtype_strings(self, hip, name, dt):
+        torch.manual_seed(0)
+        A, B = torch.randn(8, 6), torch.randn(6, 10)
+        got = trntensor.einsum("ij,jk->ik", A, B, dtype=name)
+        assert got.dtype == dt
+        np.testing.assert_allclose(got.float().numpy(), (A @ B).numpy(), atol=0.05)
+
+    def test_dtype_invalid_raises(self, hip):
+        with pytest.raises(ValueError, match="unknown dtype"):
+            trntensor.einsum("ij,jk->ik", torch.randn(4, 3), torch.randn(3, 5), dtype="foo")
+
+    def test_kahan(self, hip):
+        torch.manual_seed(42)
+        large = torch.full((1, 512), 1e6)
+        small = torch.randn(512, 1) * 1e-3
+        ref = torch.einsum("ij,jk->ik", large.double(), small.double()).float()
+        fast = trntensor.einsum("ij,jk->ik", large, small, precision="fast")
+        kahan = trntensor.einsum("ij,jk->ik", large, small, precision="kahan")
+        assert kahan.dtype == torch.float32
+        assert abs(float(kahan) - float(ref)) <= abs(float(fast) - float(ref)) + 1e-3
+
+    def test_dd_raises(self, hip):
+        with pytest.raises(NotImplementedError, match="kahan"):
+            trntensor.einsum("ij,jk->ik", torch.randn(4, 3), torch.randn(3, 5), precision="dd")
+
+    def test_fast_equals_default(self, hip):
+        torch.manual_seed(0)
+        A, B = torch.randn(8, 6), torch.randn(6, 10)
+        assert torch.equal(trntensor.einsum("ij,jk->ik", A, B), trntensor.einsum("ij,jk->ik", A, B, precision="fast"))
+
+
+class TestBackendOnDevice:
+    def test_plan_backend_is_hip(self, hip):
+        trntensor.clear_plan_cache()
+        for sub, shapes in [("ij,jk->ik", [(2048, 2048), (2048, 2048)]), ("ij,jk->ik", [(4, 3), (3, 5)]), ("ij,jk,kl->il", [(3, 4), (4, 5), (5, 2)])]:
+            p = trntensor.plan_contraction(sub, *[torch.empty(s) for s in shapes])
+            assert p.backend == "hip"
+
+    def test_pytorch_backend_refuses_to_compute(self, hip):
+        trntensor.set_backend("pytorch")
+        try:
+            with pytest.raises(RuntimeError, match="HIP kernels"):
+                trntensor.einsum("ij,jk->ik", torch.randn(4, 3), torch.randn(3, 5))
+        finally:
+            trntensor.set_backend("auto")
+
+    def test_to_device_roundtrip(self, hip):
+        t = torch.randn(3, 4)
+        d = trntensor.to_xla(t)
+        assert d.device.type == "cuda"
+        assert trntensor.from_xla(d).equal(t)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE.json configurations
+# ---------------------------------------------------------------------------
+class TestConfig1:
+    def test_df_mp2_einsum_loop(self, hip):
+        """examples/df_mp2_einsum.py:25-46 at config 1 (fp32, seed 0) with trntensor_amd.einsum."""
+        g = torch.Generator().manual_seed(0)
+        B = torch.randn(8, 32, 96, generator=g) * 0.1
+        eo = torch.sort(-20 + 19.7 * torch.rand(8, generator=g))[0]
+        ev = torch.sort(0.1 + 4.9 * torch.rand(32, generator=g))[0]
+        e = 0.0
+        for i in range(8):
+            for j in range(8):
+                T = trntensor.einsum("ap,bp->ab", B[i], B[j])
+                denom = eo[i] + eo[j] - ev.unsqueeze(1) - ev.unsqueeze(0)
+                e += (T * (2 * T - T.T) / denom).sum().item()
+        ref = cpu_ref.df_mp2_einsum_loop(B, eo, ev)
+        assert rel(e, ref) <= 1e-5
+        assert rel(trntensor.mp2_energy(B, eo, ev), ref) <= 1e-5
+
+
+class TestConfig2:
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_gemm_4096(self, hip, dt):
+        g = torch.Generator().manual_seed(0)
+        A, B, C = (torch.randn(4096, 4096, generator=g, dtype=torch.float64).to(dt) for _ in range(3))
+        got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), alpha=1.5, beta=0.5, out=C.cuda())
+        close(got.cpu(), cpu_ref.einsum("ij,jk->ik", A, B, alpha=1.5, beta=0.5, out=C))
+
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_bmm_64x512(self, hip, dt):
+        g = torch.Generator().manual_seed(0)
+        A, B, C = (torch.randn(64, 512, 512, generator=g, dtype=torch.float64).to(dt) for _ in range(3))
+        got = trntensor.einsum("bij,bjk->bik", A.cuda(), B.cuda(), alpha=1.5, beta=0.5, out=C.cuda())
+        close(got.cpu(), cpu_ref.einsum("bij,bjk->bik", A, B, alpha=1.5, beta=0.5, out=C))
+
+
+def config3_inputs():
+    g = torch.Generator().manual_seed(0)
+    C = torch.linalg.qr(torch.randn(512, 64, generator=g, dtype=torch.float64))[0]
+    E = torch.randn(512, 512, 1536, generator=g, dtype=torch.float64)
+    eri = (E + E.permute(1, 0, 2)) * (0.05 / 2**0.5)
+    return C.contiguous(), eri.contiguous()
+
+
+class TestConfig3:
+    def test_ao_to_mo_half(self, hip):
+        C, eri = config3_inputs()
+        got = trntensor.einsum("mi,mnP->inP", C.cuda(), eri.cuda())
+        assert trntensor.plan_contraction("mi,mnP->inP", C, eri).strategy == "torch"
+        close(got.cpu(), cpu_ref.ao_to_mo_half(eri, C))
+
+    def test_orthonormal_projection(self, hip):
+        """X = C^T eri; C X = C C^T eri is the projection of eri onto span(C)."""
+        C, eri = config3_inputs()
+        Cd, ed = C.cuda(), eri.cuda()
+        X = trntensor.einsum("mi,mnP->inP", Cd, ed)
+        back = trntensor.einsum("mi,inP->mnP", Cd, X)
+        proj = trntensor.einsum("mi,inP->mnP", Cd, trntensor.einsum("mi,mnP->inP", Cd, back))
+        assert normwise(proj, back) <= 1e-12
+
+
+class TestConfig5:
+    def test_greedy_path_scalar(self, hip):
+        g = torch.Generator().manual_seed(0)
+        A = torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1
+        B = torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1
+        W = torch.randn(400, 400, 800, generator=g, dtype=torch.float64) * 0.01
+        V = torch.randn(128, 128, 800, generator=g, dtype=torch.float64) * 0.1
+        plan = trntensor.plan_contraction("ia,jb,abP,ijP->", A, B, W, V)
+        assert plan.strategy == "path" and plan.contraction_path == [(0, 1), (0, 1), (0, 1)]
+        got = trntensor.einsum("ia,jb,abP,ijP->", A.cuda(), B.cuda(), W.cuda(), V.cuda())
+        # Cheap-order oracle: (ia,abP->ibP), (ibP,jb->ijP), (ijP,ijP->) in float64 on the CPU.
+        ibP = torch.einsum("ia,abP->ibP", A, W)
+        ijP = torch.einsum("ibP,jb->ijP", ibP, B)
+        ref = torch.einsum("ijP,ijP->", ijP, V)
+        scale = torch.einsum("ijP,ijP->", torch.einsum("ibP,jb->ijP", torch.einsum("ia,abP->ibP", A.abs(), W.abs()), B.abs()), V.abs())
+        assert abs(float(got) - float(ref)) / float(scale) <= 1e-14
+        assert got.shape == () and got.dtype == torch.float64

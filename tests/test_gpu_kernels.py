@@ -1,0 +1,120 @@
+"""GPU parity of the C-ABI kernels, called through the ctypes binding.
+
+tt_gemm is checked against float64 torch matmul on the CPU (the reference's
+CPU executor for the matmul/bmm strategies, trntensor/nki/dispatch.py:195-196,
+347-348) over every transpose combination, ragged edges, batching, strided
+leading dimensions and the alpha/beta epilogue. tt_strided_contract is checked
+against numpy's float64 einsum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+from tests.util import normwise
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-12, torch.float32: 1e-5}
+
+
+def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed=0):
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(seed)
+    dev = torch.device("cuda")
+    # Stored shapes (row-major) with optional extra columns to exercise ld > width.
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    A = torch.randn(batch, a_rows, a_cols + pad, generator=g, dtype=torch.float64)
+    B = torch.randn(batch, b_rows, b_cols + pad, generator=g, dtype=torch.float64)
+    C = torch.randn(batch, M, N, generator=g, dtype=torch.float64)
+    opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
+    opB = B[:, :, :b_cols].transpose(1, 2) if tb else B[:, :, :b_cols]
+    ref = alpha * torch.bmm(opA, opB)
+    if with_c:
+        ref = ref + beta * C
+    Ad, Bd, Cd = A.to(dev, dt), B.to(dev, dt), C.to(dev, dt)
+    D = torch.full((batch, M, N), float("nan"), dtype=dt, device=dev)
+    engine.gemm(
+        ta, tb, M, N, K,
+        Ad, a_cols + pad, a_rows * (a_cols + pad),
+        Bd, b_cols + pad, b_rows * (b_cols + pad),
+        D, N, M * N, batch, alpha, beta,
+        Cd if with_c else None, N, M * N,
+    )
+    torch.cuda.synchronize()
+    return normwise(D, ref)
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize(
+    "M,N,K",
+    [(1, 1, 1), (7, 5, 3), (64, 64, 16), (100, 70, 200), (129, 257, 33), (300, 40, 77), (33, 600, 130), (256, 256, 256)],
+)
+def test_gemm_layouts_and_edges(hip, dt, ta, tb, M, N, K):
+    assert _gemm_case(hip, dt, ta, tb, M, N, K, 1, 1.0, 0.0, False) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("pad", [0, 1, 3])
+def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
+    # odd leading dimensions disable the 16-byte vector path
+    assert _gemm_case(hip, dt, False, True, 70, 90, 50, 3, 1.5, 0.5, True, pad=pad, seed=1) <= TOL[dt]
+    assert _gemm_case(hip, dt, True, False, 130, 65, 40, 2, -0.75, 2.0, True, pad=pad, seed=2) <= TOL[dt]
+
+
+def test_gemm_k_zero_is_beta_c(hip):
+    assert _gemm_case(hip, torch.float64, False, False, 9, 11, 0, 2, 1.5, 0.5, True) == 0.0
+
+
+def test_gemm_rejects_bad_arguments(hip):
+    from trntensor_amd.hip import engine
+
+    A = torch.zeros(4, 4, dtype=torch.float64, device="cuda")
+    with pytest.raises(ValueError, match="leading dimension"):
+        engine.gemm(False, False, 4, 4, 4, A, 2, 0, A, 4, 0, A, 4, 0)
+    with pytest.raises(NotImplementedError, match="float32/float64"):
+        engine.gemm(False, False, 2, 2, 2, A.int(), 2, 0, A.int(), 2, 0, A.int(), 2, 0)
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize(
+    "sub,shapes",
+    [
+        ("ii->", [(37, 37)]),
+        ("ij->ji", [(33, 65)]),
+        ("ijk->kj", [(5, 7, 9)]),
+        ("i,i->", [(100003,)]),
+        ("i,j->ij", [(130,), (70,)]),
+        ("ij,ij->ij", [(40, 50), (40, 50)]),
+        ("ij,jk->i", [(20, 30), (30, 10)]),
+        ("bij,bjk->bik", [(3, 4, 5), (3, 5, 6)]),
+        ("iajb,abij->", [(6, 5, 7, 4), (5, 4, 6, 7)]),
+    ],
+)
+def test_strided_contract_vs_numpy(hip, dt, sub, shapes):
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(3)
+    ops = [torch.randn(*s, generator=g, dtype=torch.float64) for s in shapes]
+    ref = torch.from_numpy(np.asarray(brute.einsum_f64(sub, *[o.numpy() for o in ops])))
+    lhs, out = sub.split("->")
+    res = engine.contract(lhs.split(","), out, [o.to("cuda", dt) for o in ops])
+    torch.cuda.synchronize()
+    assert normwise(res, ref) <= (1e-12 if dt == torch.float64 else 1e-5)
+
+
+def test_strided_split_reduction_matches_single_pass(hip):
+    """A reduction long enough to use partials agrees with float64 numpy."""
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(3, 2_000_000, generator=g, dtype=torch.float64)
+    y = torch.randn(3, 2_000_000, generator=g, dtype=torch.float64)
+    res = engine.contract(["ij", "ij"], "i", [x.cuda(), y.cuda()])
+    ref = (x * y).sum(1)
+    assert normwise(res, ref) <= 1e-12

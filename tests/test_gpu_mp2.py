@@ -1,0 +1,140 @@
+"""GPU parity of the fused DF-MP2 energy (tt_mp2_energy via trntensor_amd.mp2_energy).
+
+Oracle: the reference's CPU loop restated in oracle/cpu_ref.py (quantum.py:87-100),
+pinned in tests/test_oracle.py. Bars (north star): relative error <= 1e-10 in
+float64, <= 1e-5 in float32. At the full config-4 size the oracle itself runs
+(about 1 TFLOP of CPU GEMMs); properties the mathematics fixes (shift
+invariance, quartic scaling, virtual relabelling) are checked on the GPU
+result alone.
+"""
+
+import pytest
+import torch
+
+import trntensor_amd as tt
+from oracle import brute, cpu_ref
+from tests.util import rel
+
+pytestmark = pytest.mark.gpu
+
+
+def inputs(nocc, nvir, naux, dtype=torch.float64, seed=0, scale=0.05):
+    """Config-4 recipe: B ~ N(0, scale^2), e_occ ~ U(-20, -0.3), e_vir ~ U(0.1, 5), sorted."""
+    g = torch.Generator().manual_seed(seed)
+    B = torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64) * scale
+    eo = torch.sort(-20 + 19.7 * torch.rand(nocc, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(nvir, generator=g, dtype=torch.float64))[0]
+    return B.to(dtype), eo.to(dtype), ev.to(dtype)
+
+
+SHAPES = [
+    (1, 1, 1),
+    (2, 3, 5),
+    (5, 19, 72),
+    (8, 32, 96),
+    (3, 64, 16),
+    (4, 70, 33),
+    (3, 128, 100),
+    (6, 130, 17),
+    (2, 200, 50),
+    (5, 97, 130),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_mp2_fp64_matches_oracle(hip, shape):
+    B, eo, ev = inputs(*shape, seed=sum(shape))
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert got.dtype == torch.float64 and got.shape == () and got.device.type == "cuda"
+    assert rel(got, ref) <= 1e-10
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_mp2_fp32_matches_oracle(hip, shape):
+    B, eo, ev = inputs(*shape, dtype=torch.float32, seed=sum(shape) + 1)
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert got.dtype == torch.float32
+    assert rel(got, ref) <= 1e-5
+
+
+def test_mp2_cpu_tensors_round_trip(hip):
+    """CPU operands are staged through the device; the result comes back on the CPU."""
+    B, eo, ev = inputs(4, 40, 24, seed=9)
+    got = tt.mp2_energy(B, eo, ev)
+    assert got.device.type == "cpu"
+    assert rel(got, brute.mp2_energy_4index(B, eo, ev)) <= 1e-12
+
+
+def test_mp2_tutorial_known_answer(hip):
+    """docs/tutorial_df_mp2.md: E = -50.5432928801 for the example recipe (seed 42)."""
+    torch.manual_seed(42)
+    B = torch.randn(5, 19, 72) * 0.1
+    eo = -torch.sort(torch.rand(5))[0] - 0.5
+    ev = torch.sort(torch.rand(19))[0] + 0.1
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert abs(float(got) - (-50.5432928801)) <= 5e-4  # fp32 inputs, fp32 per-element terms
+    got64 = tt.mp2_energy(B.double().cuda(), eo.double().cuda(), ev.double().cuda())
+    assert abs(float(got64) - brute.mp2_energy_4index(B, eo, ev)) <= 1e-10 * 51
+
+
+def test_mp2_atomic_mode_matches_deterministic(hip):
+    B, eo, ev = inputs(12, 150, 64, seed=5)
+    B, eo, ev = B.cuda(), eo.cuda(), ev.cuda()
+    det = hip._hip_mp2_energy(B, eo, ev, deterministic=True)
+    det2 = hip._hip_mp2_energy(B, eo, ev, deterministic=True)
+    atom = hip._hip_mp2_energy(B, eo, ev, deterministic=False)
+    assert float(det) == float(det2)  # fixed summation order: bitwise repeatable
+    assert rel(atom, det) <= 1e-13
+
+
+def test_mp2_zero_and_empty(hip):
+    B = torch.zeros(3, 10, 7, dtype=torch.float64, device="cuda")
+    eo = -torch.ones(3, dtype=torch.float64, device="cuda")
+    ev = torch.ones(10, dtype=torch.float64, device="cuda")
+    assert float(tt.mp2_energy(B, eo, ev)) == 0.0
+    Bz = torch.zeros(0, 10, 7, dtype=torch.float64, device="cuda")
+    assert float(tt.mp2_energy(Bz, eo[:0], ev)) == 0.0
+
+
+def test_mp2_shape_errors_match_reference(hip):
+    B3 = torch.randn(3, 4, 5, device="cuda")
+    with pytest.raises(ValueError, match="must be 3D"):
+        tt.mp2_energy(torch.randn(3, 4), torch.randn(3), torch.randn(4))
+    with pytest.raises(ValueError, match="eps_occ"):
+        tt.mp2_energy(B3, torch.randn(2), torch.randn(4))
+    with pytest.raises(ValueError, match="eps_vir"):
+        tt.mp2_energy(B3, torch.randn(3), torch.randn(5))
+
+
+@pytest.fixture(scope="module")
+def config4():
+    return inputs(64, 320, 1200, seed=0)
+
+
+def test_mp2_config4_fp64_matches_oracle(hip, config4):
+    B, eo, ev = config4
+    torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert rel(got, ref) <= 1e-10, (float(got), float(ref))
+
+
+def test_mp2_config4_fp32_matches_oracle(hip, config4):
+    B, eo, ev = (x.float() for x in config4)
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert rel(got, ref) <= 1e-5, (float(got), float(ref))
+
+
+def test_mp2_config4_invariants(hip, config4):
+    """Uniform shift of every orbital energy leaves every denominator unchanged;
+    E(cB) = c^4 E(B); relabelling virtuals (B[:, pi], e_vir[pi]) leaves E unchanged."""
+    B, eo, ev = (x.cuda() for x in config4)
+    e0 = float(tt.mp2_energy(B, eo, ev))
+    assert rel(tt.mp2_energy(B, eo + 0.5, ev + 0.5), e0) <= 1e-11
+    assert rel(tt.mp2_energy(2.0 * B, eo, ev), 16.0 * e0) <= 1e-13
+    perm = torch.randperm(B.shape[1], generator=torch.Generator().manual_seed(1)).cuda()
+    assert rel(tt.mp2_energy(B[:, perm].contiguous(), eo, ev[perm]), e0) <= 1e-11
+    assert e0 < 0.0

@@ -1,0 +1,190 @@
+"""Pins for the CPU oracle (oracle/cpu_ref.py), on any host.
+
+Each oracle function is checked against something it does not share code
+with: the reference's tutorial known answer, the golden fixtures (explicit
+loops / numpy float64), closed forms and invariances. The planted-mistake
+tests show the pins reject a dropped exchange term, a wrong sign, a
+transposed operand and a wrong denominator order.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute, cpu_ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+# ---------------------------------------------------------------------------
+# MP2
+# ---------------------------------------------------------------------------
+def test_tutorial_known_answer():
+    """docs/tutorial_df_mp2.md:23-28,75-77 / examples/df_mp2_einsum.py:64-67:
+    E = -50.5432928801 for nocc,nvir,naux = 5,19,72, seed 42."""
+    torch.manual_seed(42)
+    B = torch.randn(5, 19, 72) * 0.1
+    eo = -torch.sort(torch.rand(5))[0] - 0.5
+    ev = torch.sort(torch.rand(19))[0] + 0.1
+    e = cpu_ref.df_mp2_einsum_loop(B, eo, ev)
+    assert abs(e - (-50.5432928801)) <= 5e-11
+    assert abs(float(cpu_ref.mp2_energy(B, eo, ev)) - e) <= 1e-4
+
+
+def test_mp2_matches_golden_loops():
+    g = load("mp2_small.npz")
+    k = 0
+    while f"B{k}" in g:
+        B, eo, ev = (torch.from_numpy(g[n + str(k)]) for n in ("B", "eo", "ev"))
+        e = float(cpu_ref.mp2_energy(B, eo, ev))
+        assert abs(e - float(g[f"E_loops{k}"])) <= 1e-12 * max(1.0, abs(e))
+        assert abs(e - float(g[f"E_4index{k}"])) <= 1e-12 * max(1.0, abs(e))
+        k += 1
+    assert k == 5
+
+
+def test_mp2_matches_reference_unrolled_formula():
+    """tests/test_quantum.py:11-33: the loop equals the 4-index einsum formula."""
+    torch.manual_seed(0)
+    B = torch.randn(2, 3, 5) * 0.1
+    eo = torch.tensor([-0.5, -0.4])
+    ev = torch.tensor([0.1, 0.2, 0.3])
+    T = torch.einsum("iap,jbp->ijab", B, B)
+    denom = eo.view(-1, 1, 1, 1) + eo.view(1, -1, 1, 1) - ev.view(1, 1, -1, 1) - ev.view(1, 1, 1, -1)
+    expected = (T * (2 * T - T.transpose(-1, -2)) / denom).sum()
+    torch.testing.assert_close(cpu_ref.mp2_energy(B, eo, ev), expected, atol=1e-6, rtol=1e-6)
+
+
+def test_mp2_rank1_closed_form():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4, generator=g, dtype=torch.float64)
+    y = torch.randn(6, generator=g, dtype=torch.float64)
+    eo = torch.sort(-20 + 19.7 * torch.rand(4, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(6, generator=g, dtype=torch.float64))[0]
+    B = (x[:, None] * y[None, :])[:, :, None]
+    e = float(cpu_ref.mp2_energy(B, eo, ev))
+    assert abs(e - brute.mp2_energy_rank1(x, y, eo, ev)) <= 1e-13 * abs(e)
+
+
+def test_mp2_invariants():
+    g = torch.Generator().manual_seed(6)
+    B = torch.randn(3, 7, 9, generator=g, dtype=torch.float64) * 0.1
+    eo = torch.sort(-20 + 19.7 * torch.rand(3, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(7, generator=g, dtype=torch.float64))[0]
+    e = float(cpu_ref.mp2_energy(B, eo, ev))
+    assert e < 0
+    assert abs(float(cpu_ref.mp2_energy(B, eo + 0.5, ev + 0.5)) - e) <= 1e-12 * abs(e)
+    assert abs(float(cpu_ref.mp2_energy(3.0 * B, eo, ev)) - 81.0 * e) <= 1e-12 * 81 * abs(e)
+    perm = torch.randperm(7, generator=g)
+    assert abs(float(cpu_ref.mp2_energy(B[:, perm], eo, ev[perm])) - e) <= 1e-12 * abs(e)
+    assert float(cpu_ref.mp2_energy(torch.zeros_like(B), eo, ev)) == 0.0
+
+
+def _mutant(kind):
+    """Oracle loop with one planted mistake (CPU only)."""
+
+    def run(B, eo, ev):
+        e = B.new_zeros(())
+        for i in range(B.shape[0]):
+            for j in range(B.shape[0]):
+                Bj = B[j] if kind != "transposed" else B[i]
+                T = torch.einsum("ap,bp->ab", B[i], Bj)
+                if kind == "denominator":
+                    d = eo[i] + eo[j] - ev.unsqueeze(1) + ev.unsqueeze(0)
+                else:
+                    d = eo[i] + eo[j] - ev.unsqueeze(1) - ev.unsqueeze(0)
+                if kind == "no_exchange":
+                    num = T * (2 * T)
+                elif kind == "sign":
+                    num = T * (2 * T + T.T)
+                else:
+                    num = T * (2 * T - T.T)
+                e = e + (num / d).sum()
+        return e
+
+    return run
+
+
+@pytest.mark.parametrize("kind", ["no_exchange", "sign", "transposed", "denominator"])
+def test_planted_mistakes_fail_the_golden_pin(kind):
+    g = load("mp2_small.npz")
+    worst = 0.0
+    for k in range(1, 5):
+        B, eo, ev = (torch.from_numpy(g[n + str(k)]) for n in ("B", "eo", "ev"))
+        ref = float(g[f"E_loops{k}"])
+        worst = max(worst, abs(float(_mutant(kind)(B, eo, ev)) - ref) / abs(ref))
+    assert worst > 1e-6
+
+
+# ---------------------------------------------------------------------------
+# AO -> MO
+# ---------------------------------------------------------------------------
+def test_ao_to_mo_matches_golden_and_two_step():
+    g = load("ao2mo_small.npz")
+    for k in range(2):
+        eri, Co, Cv = (torch.from_numpy(g[n + str(k)]) for n in ("eri", "Co", "Cv"))
+        ref = g[f"B{k}"]
+        np.testing.assert_allclose(cpu_ref.ao_to_mo_transform(eri, Co, Cv).numpy(), ref, rtol=0, atol=1e-13)
+        np.testing.assert_allclose(cpu_ref.ao_to_mo_two_step(eri, Co, Cv).numpy(), ref, rtol=0, atol=1e-13)
+        X = cpu_ref.ao_to_mo_half(eri, Co)
+        np.testing.assert_allclose(X.numpy(), np.einsum("mi,mnP->inP", g[f"Co{k}"], g[f"eri{k}"]), atol=1e-13)
+
+
+# ---------------------------------------------------------------------------
+# einsum and the executors
+# ---------------------------------------------------------------------------
+def test_einsum_matches_golden_numpy():
+    g = load("einsum_small.npz")
+    k = 0
+    while f"sub{k}" in g:
+        sub = str(g[f"sub{k}"])
+        ops, m = [], 0
+        while f"op{k}_{m}" in g:
+            ops.append(torch.from_numpy(g[f"op{k}_{m}"]))
+            m += 1
+        got = cpu_ref.einsum(sub, *ops)
+        np.testing.assert_allclose(got.numpy(), g[f"out{k}"], rtol=1e-12, atol=1e-12)
+        k += 1
+    assert k == 9
+
+
+def test_alpha_beta_closed_form():
+    g = torch.Generator().manual_seed(1)
+    A, B, C = (torch.randn(*s, generator=g, dtype=torch.float64) for s in [(4, 3), (3, 5), (4, 5)])
+    got = cpu_ref.einsum("ij,jk->ik", A, B, alpha=2.0, beta=0.5, out=C)
+    torch.testing.assert_close(got, 2.0 * (A @ B) + 0.5 * C)
+
+
+def test_dtype_and_precision_semantics():
+    A, B = torch.randn(4, 3), torch.randn(3, 5)
+    assert cpu_ref.einsum("ij,jk->ik", A, B, dtype="bf16").dtype == torch.bfloat16
+    assert cpu_ref.einsum("ij,jk->ik", A, B, precision="kahan").dtype == torch.float32
+    with pytest.raises(ValueError, match="unknown dtype"):
+        cpu_ref.einsum("ij,jk->ik", A, B, dtype="fp64")
+    with pytest.raises(NotImplementedError, match="kahan"):
+        cpu_ref.einsum("ij,jk->ik", A, B, precision="dd")
+
+
+def test_path_step_naming():
+    """trntensor/einsum.py:171-185 on the config-5 expression: 'iajb' then 'abij'."""
+    terms = ["ia", "jb", "abP", "ijP"]
+    assert cpu_ref.path_step_output(terms, 0, 1, "") == "iajb"
+    assert cpu_ref.path_step_output(["abP", "ijP", "iajb"], 0, 1, "") == "abij"
+
+
+def test_misplanned_detection():
+    A, B = torch.randn(3, 4), torch.randn(4, 5)
+    assert not cpu_ref.misplanned_by_reference("ij,jk->ik", A, B)
+    assert cpu_ref.misplanned_by_reference("ij,jk->ki", A, B)
+    assert cpu_ref.misplanned_by_reference("ij,jk->i", A, B)
+    assert not cpu_ref.misplanned_by_reference("bij,bjk->bik", torch.randn(2, 3, 4), torch.randn(2, 4, 5))
+    assert cpu_ref.misplanned_by_reference("iap,ibp->iab", torch.randn(2, 3, 4), torch.randn(2, 5, 4))
+    # the reference's own result differs from einsum semantics here
+    res = cpu_ref.einsum("ij,jk->ki", torch.eye(3) * 2, torch.arange(9.0).view(3, 3))
+    assert not torch.equal(res, torch.einsum("ij,jk->ki", torch.eye(3) * 2, torch.arange(9.0).view(3, 3)))

@@ -1,0 +1,315 @@
+// MFMA GEMM core for gfx950: batched, strided, transposed operands in place,
+// fused alpha/beta epilogue. fp64 on v_mfma_f64_16x16x4f64, fp32 on
+// v_mfma_f32_16x16x4f32.
+//
+// Workgroup: 256 threads = 4 wavefronts, output tile BM x BN, each wavefront
+// a 64x64 sub-tile (4 x 4 MFMA blocks, 64 accumulators per lane).
+// K advances in stages of 16 through two LDS buffers: while the MFMAs consume
+// one stage, the next stage's global loads are in flight in registers and are
+// written to the other buffer afterwards (one barrier per stage).
+//
+// LDS layouts follow the operand's contiguous direction so every global load
+// and LDS store is a 16-byte vector:
+//   k-contiguous operand   -> [row][k],  row pitch 16 + 16 B of padding
+//   row-contiguous operand -> [k][row],  k-row pitch ROWS + 16 B of padding
+// Inside a 16-wide stage, MFMA step s (0..3) gives lane-group g = lane / 16
+// the k index 4 g + s for both operands, so a lane's four k values are
+// adjacent in the [row][k] layout and one 32-byte read feeds four MFMAs.
+#include "tt_common.hpp"
+
+namespace tt {
+
+constexpr int kBK = 16;
+constexpr int kThreads = 256;
+
+struct GemmArgs {
+    const void* A;
+    const void* B;
+    const void* C;
+    void* D;
+    int64_t M, N, K;
+    int64_t lda, ldb, ldc, ldd;
+    int64_t sA, sB, sC, sD;
+    int64_t batch;
+    int64_t tiles_m, tiles_n;
+    double alpha, beta;
+};
+
+// One operand's ROWS x 16 stage: global -> registers -> LDS, plus fragment reads.
+// KC: element (row, k) at p[row * ld + k]; otherwise at p[k * ld + row].
+template <typename T, int ROWS, bool KC, bool VEC>
+struct Stage {
+    static constexpr int V = Vec16<T>::n;
+    static constexpr int PAD = 16 / sizeof(T);
+    static constexpr int PITCH = KC ? (kBK + PAD) : (ROWS + PAD);
+    static constexpr int ELEMS = KC ? ROWS * PITCH : kBK * PITCH;
+    static constexpr int NVEC = ROWS * kBK / V;
+    static constexpr int PER_THREAD = NVEC / kThreads;
+    static_assert(NVEC % kThreads == 0, "tile must split evenly over the workgroup");
+    typedef typename Vec16<T>::type vec_t;
+
+    vec_t reg[PER_THREAD];
+
+    // Position of vector `v` inside the tile.
+    __device__ __forceinline__ static void place(int v, int& row, int& k) {
+        if (KC) {
+            row = v / (kBK / V);
+            k = (v % (kBK / V)) * V;
+        } else {
+            k = v / (ROWS / V);
+            row = (v % (ROWS / V)) * V;
+        }
+    }
+
+    __device__ __forceinline__ void load(const T* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
+                                         int64_t k0, int64_t kdim) {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            int r, k;
+            place(it * kThreads + threadIdx.x, r, k);
+            const int64_t gr = row0 + r;
+            const int64_t gk = k0 + k;
+            if (KC) {
+                const T* src = p + gr * ld + gk;
+                if (VEC && gr < rows && gk + V <= kdim) {
+                    reg[it] = *reinterpret_cast<const vec_t*>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) reg[it][e] = (gr < rows && gk + e < kdim) ? src[e] : T(0);
+                }
+            } else {
+                const T* src = p + gk * ld + gr;
+                if (VEC && gk < kdim && gr + V <= rows) {
+                    reg[it] = *reinterpret_cast<const vec_t*>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) reg[it][e] = (gk < kdim && gr + e < rows) ? src[e] : T(0);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(T* s) const {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            int r, k;
+            place(it * kThreads + threadIdx.x, r, k);
+            T* dst = KC ? (s + r * PITCH + k) : (s + k * PITCH + r);
+            *reinterpret_cast<vec_t*>(dst) = reg[it];
+        }
+    }
+
+    // The four k values (MFMA steps 0..3) this lane feeds for the 16-row block at rb.
+    __device__ __forceinline__ static void frag(const T* s, int rb, int lane, T out[4]) {
+        const int r = rb + (lane & 15);
+        const int g = lane >> 4;
+        if (KC) {
+            const vec_t* q = reinterpret_cast<const vec_t*>(s + r * PITCH + 4 * g);
+            if (V == 2) {
+                vec_t x0 = q[0], x1 = q[1];
+                out[0] = x0[0];
+                out[1] = x0[1];
+                out[2] = x1[0];
+                out[3] = x1[1];
+            } else {
+                vec_t x = q[0];
+                out[0] = x[0];
+                out[1] = x[1];
+                out[2] = x[2];
+                out[3] = x[3];
+            }
+        } else {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) out[st] = s[(4 * g + st) * PITCH + r];
+        }
+    }
+};
+
+template <typename T, int BM, int BN, bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
+    typedef Mfma<T> MF;
+    typedef typename MF::acc_t acc_t;
+    // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
+    typedef Stage<T, BM, !TA, VEC> SA;
+    typedef Stage<T, BN, TB, VEC> SB;
+    constexpr int WAVES_N = BN / 64;
+    static_assert((BM / 64) * WAVES_N == 4, "four 64x64 wavefront tiles per workgroup");
+
+    __shared__ __attribute__((aligned(16))) T lds[2 * (SA::ELEMS + SB::ELEMS)];
+    // Stage buffers: A0 A1 B0 B1.
+    auto bufA = [&](int b) -> T* { return lds + b * SA::ELEMS; };
+    auto bufB = [&](int b) -> T* { return lds + 2 * SA::ELEMS + b * SB::ELEMS; };
+
+    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t total = tiles * g.batch;
+    const int64_t id = xcd_remap(blockIdx.x, total);
+    const int64_t bat = id / tiles;
+    int64_t t = id - bat * tiles;
+    // Grouped order: 8 tile-rows sweep each tile-column, so concurrently
+    // running workgroups share A panels and B panels.
+    constexpr int64_t GROUP = 8;
+    const int64_t grp = t / (GROUP * g.tiles_n);
+    const int64_t first_m = grp * GROUP;
+    const int64_t gsize = min(g.tiles_m - first_m, GROUP);
+    const int64_t rem = t - grp * GROUP * g.tiles_n;
+    const int64_t tm = first_m + rem % gsize;
+    const int64_t tn = rem / gsize;
+    const int64_t m0 = tm * BM;
+    const int64_t n0 = tn * BN;
+
+    const T* A = static_cast<const T*>(g.A) + bat * g.sA;
+    const T* B = static_cast<const T*>(g.B) + bat * g.sB;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / WAVES_N) * 64;
+    const int wn0 = (wave % WAVES_N) * 64;
+
+    acc_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+
+    SA sa;
+    SB sb;
+    const int64_t nk = (g.K + kBK - 1) / kBK;
+    if (nk > 0) {
+        sa.load(A, g.lda, m0, g.M, 0, g.K);
+        sb.load(B, g.ldb, n0, g.N, 0, g.K);
+        sa.store(bufA(0));
+        sb.store(bufB(0));
+    }
+    __syncthreads();
+
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            sa.load(A, g.lda, m0, g.M, (kt + 1) * kBK, g.K);
+            sb.load(B, g.ldb, n0, g.N, (kt + 1) * kBK, g.K);
+        }
+        T fa[4][4], fb[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) SA::frag(bufA(cur), wm0 + 16 * i, lane, fa[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) SB::frag(bufB(cur), wn0 + 16 * j, lane, fb[j]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
+        if (more) {
+            sa.store(bufA(cur ^ 1));
+            sb.store(bufB(cur ^ 1));
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: D = alpha * acc (+ beta * C), masked at the matrix edge.
+    const T alpha = (T)g.alpha;
+    const T beta = (T)g.beta;
+    const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
+    T* D = static_cast<T*>(g.D) + bat * g.sD;
+    const int col_l = lane & 15;
+    const int row_l = 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t col = n0 + wn0 + 16 * j + col_l;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm0 + 16 * i + row_l + r;
+                if (row < g.M && col < g.N) {
+                    T v = acc[i][j][r];
+                    if (g.alpha != 1.0) v = alpha * v;
+                    if (C) v = v + beta * C[row * g.ldc + col];
+                    D[row * g.ldd + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <typename T, int BM, int BN>
+static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) {
+    g.tiles_m = (g.M + BM - 1) / BM;
+    g.tiles_n = (g.N + BN - 1) / BN;
+    const int64_t total = g.tiles_m * g.tiles_n * g.batch;
+    if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
+    dim3 grid((unsigned)total), block(kThreads);
+#define TT_GEMM_CASE(TA, TB, VC) \
+    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, TA, TB, VC>), grid, block, 0, st, g);
+    TT_GEMM_CASE(false, false, false)
+    TT_GEMM_CASE(false, false, true)
+    TT_GEMM_CASE(false, true, false)
+    TT_GEMM_CASE(false, true, true)
+    TT_GEMM_CASE(true, false, false)
+    TT_GEMM_CASE(true, false, true)
+    TT_GEMM_CASE(true, true, false)
+    TT_GEMM_CASE(true, true, true)
+#undef TT_GEMM_CASE
+    return check_launch("tt_gemm");
+}
+
+template <typename T>
+static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
+    constexpr int V = Vec16<T>::n;
+    auto ok16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    // 16-byte vectors need aligned bases, leading dimensions and batch strides.
+    bool vec = ok16(g.A) && ok16(g.B) && g.lda % V == 0 && g.ldb % V == 0;
+    if (g.batch > 1) vec = vec && g.sA % V == 0 && g.sB % V == 0;
+    if (g.M <= 64) return launch_tile<T, 64, 256>(g, ta, tb, vec, st);
+    if (g.N <= 64) return launch_tile<T, 256, 64>(g, ta, tb, vec, st);
+    return launch_tile<T, 128, 128>(g, ta, tb, vec, st);
+}
+
+int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
+    if (dtype == TT_F64) return gemm_typed<double>(g, ta, tb, st);
+    if (dtype == TT_F32) return gemm_typed<float>(g, ta, tb, st);
+    return set_error(TT_UNSUPPORTED, "tt_gemm: dtype %d (only TT_F32, TT_F64)", dtype);
+}
+
+}  // namespace tt
+
+extern "C" int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K, double alpha,
+                       const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB,
+                       double beta, const void* C, int64_t ldc, int64_t strideC, void* D, int64_t ldd,
+                       int64_t strideD, int64_t batch, void* stream) {
+    using namespace tt;
+    if (M < 0 || N < 0 || K < 0 || batch < 0)
+        return set_error(TT_INVALID, "tt_gemm: negative extent (M=%lld N=%lld K=%lld batch=%lld)", (long long)M,
+                         (long long)N, (long long)K, (long long)batch);
+    if (M == 0 || N == 0 || batch == 0) return TT_OK;
+    if (!D) return set_error(TT_INVALID, "tt_gemm: D is NULL");
+    if (K > 0 && (!A || !B)) return set_error(TT_INVALID, "tt_gemm: A or B is NULL");
+    const int64_t rowsA = transA ? K : M, colsA = transA ? M : K;
+    const int64_t rowsB = transB ? N : K, colsB = transB ? K : N;
+    if (K > 0 && ((rowsA > 1 && lda < colsA) || (rowsB > 1 && ldb < colsB)))
+        return set_error(TT_INVALID, "tt_gemm: leading dimension smaller than a row (lda=%lld ldb=%lld)",
+                         (long long)lda, (long long)ldb);
+    if ((M > 1 && ldd < N) || (C && M > 1 && ldc < N))
+        return set_error(TT_INVALID, "tt_gemm: ldd/ldc smaller than N");
+    GemmArgs g;
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.D = D;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    g.ldd = ldd;
+    g.sA = strideA;
+    g.sB = strideB;
+    g.sC = strideC;
+    g.sD = strideD;
+    g.batch = batch;
+    g.alpha = alpha;
+    g.beta = beta;
+    return gemm_dispatch(dtype, transA != 0, transB != 0, g, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,344 @@
+// Fused DF-MP2 correlation energy for gfx950.
+//
+//   E = sum_{ij} sum_{ab} T_ab (2 T_ab - T_ba) / (e_i + e_j - e_a - e_b),
+//   T = T^{ij} = B_i B_j^T,  B_i = B[i] : (nvir, naux), P contiguous.
+//
+// Work unit: occupied pair i <= j and virtual 64-blocks p <= q. Because
+// T^{ij}_{ba} = (B_j[p] B_i[q]^T)_{ab} for a in block p and b in block q,
+// one workgroup forms
+//   X = B_i[p] B_j[q]^T    (T_ab for a in p, b in q)
+//   Y = B_j[p] B_i[q]^T    (T_ba at the same (a, b) position)
+// on MFMA in the same register layout, so the exchange term pairs X and Y
+// element by element with no transpose. For p < q the unit also accounts for
+// the mirrored block (q, p), whose terms are Y (2Y - X) / Delta_ba. For i = j,
+// Y equals X and is not recomputed. For i < j the unit's sum is doubled,
+// since the (j, i) pair contributes the same amount (Delta is symmetric).
+// T never leaves registers; each workgroup reduces to one double with
+// wavefront shuffles and either stores it (deterministic mode, summed later
+// in a fixed order) or adds it with one atomic.
+//
+// Per-element arithmetic follows the reference's operation order
+// (trntensor/quantum.py:97-99): denominator ((e_i + e_j) - e_a) - e_b with a
+// the row index, term (T * (2T - T^T)) / denominator with IEEE division, in
+// the input dtype; the energy is accumulated in double.
+#include "tt_common.hpp"
+
+namespace tt {
+
+constexpr int kMp2BK = 16;
+constexpr int kMp2Threads = 256;
+constexpr int kMp2Tile = 64;
+
+template <typename T, bool VEC>
+struct Panel {
+    // 64 rows x 16 k of one B_i block, k contiguous in memory and in LDS.
+    static constexpr int V = Vec16<T>::n;
+    static constexpr int PITCH = kMp2BK + 16 / sizeof(T);
+    static constexpr int ELEMS = kMp2Tile * PITCH;
+    static constexpr int PER_THREAD = kMp2Tile * kMp2BK / V / kMp2Threads;
+    static_assert(PER_THREAD >= 1, "panel split");
+    typedef typename Vec16<T>::type vec_t;
+
+    vec_t reg[PER_THREAD];
+
+    __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            const int v = it * kMp2Threads + threadIdx.x;
+            const int r = v / (kMp2BK / V);
+            const int k = (v % (kMp2BK / V)) * V;
+            const int64_t gk = k0 + k;
+            const T* src = base + (int64_t)r * naux + gk;
+            if (VEC && r < rows && gk + V <= naux) {
+                reg[it] = *reinterpret_cast<const vec_t*>(src);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) reg[it][e] = (r < rows && gk + e < naux) ? src[e] : T(0);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(T* s) const {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            const int v = it * kMp2Threads + threadIdx.x;
+            const int r = v / (kMp2BK / V);
+            const int k = (v % (kMp2BK / V)) * V;
+            *reinterpret_cast<vec_t*>(s + r * PITCH + k) = reg[it];
+        }
+    }
+
+    // Lane's four k values (MFMA steps 0..3: k = 4 g + step) for rows rb..rb+15.
+    __device__ __forceinline__ static void frag(const T* s, int rb, int lane, T out[4]) {
+        const vec_t* q = reinterpret_cast<const vec_t*>(s + (rb + (lane & 15)) * PITCH + 4 * (lane >> 4));
+        if (V == 2) {
+            vec_t x0 = q[0], x1 = q[1];
+            out[0] = x0[0];
+            out[1] = x0[1];
+            out[2] = x1[0];
+            out[3] = x1[1];
+        } else {
+            vec_t x = q[0];
+            out[0] = x[0];
+            out[1] = x[1];
+            out[2] = x[2];
+            out[3] = x[3];
+        }
+    }
+};
+
+struct Mp2Args {
+    const void* B;
+    const void* eo;
+    const void* ev;
+    double* partial;  // one per workgroup (deterministic) or nullptr
+    double* accum;    // atomic accumulator (non-deterministic) or nullptr
+    int64_t naux;
+    int nocc, nvir, nblk;
+    int64_t npq;     // nblk * (nblk + 1) / 2
+    int64_t ntasks;  // npq * nocc * (nocc + 1) / 2
+};
+
+// Index of (x, y), x <= y < n, in row-major upper-triangle order -> (x, y).
+__device__ __forceinline__ void tri_decode(int64_t idx, int n, int& x, int& y) {
+    int r = 0;
+    while (idx >= n - r) {
+        idx -= n - r;
+        ++r;
+    }
+    x = r;
+    y = r + (int)idx;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
+    typedef Mfma<T> MF;
+    typedef typename MF::acc_t acc_t;
+    typedef Panel<T, VEC> PN;
+
+    __shared__ __attribute__((aligned(16))) T lds[2][4][PN::ELEMS];
+    __shared__ double red[4];
+
+    const int64_t task = xcd_remap(blockIdx.x, g.ntasks);
+    const int64_t pair = task / g.npq;
+    const int64_t u = task - pair * g.npq;
+    int i, j, p, q;
+    tri_decode(pair, g.nocc, i, j);
+    tri_decode(u, g.nblk, p, q);
+    const bool same = (i == j);
+
+    const T* B = static_cast<const T*>(g.B);
+    const int64_t nvir = g.nvir;
+    const int rows_p = min(kMp2Tile, g.nvir - p * kMp2Tile);
+    const int rows_q = min(kMp2Tile, g.nvir - q * kMp2Tile);
+    // Panels: 0 = B_i[p], 1 = B_j[q], 2 = B_j[p], 3 = B_i[q].
+    const T* base0 = B + ((int64_t)i * nvir + (int64_t)p * kMp2Tile) * g.naux;
+    const T* base1 = B + ((int64_t)j * nvir + (int64_t)q * kMp2Tile) * g.naux;
+    const T* base2 = B + ((int64_t)j * nvir + (int64_t)p * kMp2Tile) * g.naux;
+    const T* base3 = B + ((int64_t)i * nvir + (int64_t)q * kMp2Tile) * g.naux;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wr = (wave >> 1) * 32;  // quadrant row offset (a within p)
+    const int wc = (wave & 1) * 32;   // quadrant col offset (b within q)
+
+    acc_t X[2][2], Y[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            X[a][b] = acc_t{0, 0, 0, 0};
+            Y[a][b] = acc_t{0, 0, 0, 0};
+        }
+
+    PN s0, s1, s2, s3;
+    const int64_t nk = (g.naux + kMp2BK - 1) / kMp2BK;
+    s0.load(base0, rows_p, g.naux, 0);
+    s1.load(base1, rows_q, g.naux, 0);
+    if (!same) {
+        s2.load(base2, rows_p, g.naux, 0);
+        s3.load(base3, rows_q, g.naux, 0);
+    }
+    s0.store(lds[0][0]);
+    s1.store(lds[0][1]);
+    if (!same) {
+        s2.store(lds[0][2]);
+        s3.store(lds[0][3]);
+    }
+    __syncthreads();
+
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        const int64_t k1 = (kt + 1) * kMp2BK;
+        if (more) {
+            s0.load(base0, rows_p, g.naux, k1);
+            s1.load(base1, rows_q, g.naux, k1);
+            if (!same) {
+                s2.load(base2, rows_p, g.naux, k1);
+                s3.load(base3, rows_q, g.naux, k1);
+            }
+        }
+        T f0[2][4], f1[2][4];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) PN::frag(lds[cur][0], wr + 16 * a, lane, f0[a]);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) PN::frag(lds[cur][1], wc + 16 * b, lane, f1[b]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
+        if (!same) {
+            T f2[2][4], f3[2][4];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) PN::frag(lds[cur][2], wr + 16 * a, lane, f2[a]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) PN::frag(lds[cur][3], wc + 16 * b, lane, f3[b]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
+        }
+        if (more) {
+            s0.store(lds[cur ^ 1][0]);
+            s1.store(lds[cur ^ 1][1]);
+            if (!same) {
+                s2.store(lds[cur ^ 1][2]);
+                s3.store(lds[cur ^ 1][3]);
+            }
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: denominators and exchange term in registers.
+    const T* eo = static_cast<const T*>(g.eo);
+    const T* ev = static_cast<const T*>(g.ev);
+    const T eij = eo[i] + eo[j];
+    const bool mirror = (p != q);
+    double sum = 0.0;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int cb = wc + 16 * b + (lane & 15);
+        const int vb = q * kMp2Tile + cb;
+        const bool okb = cb < rows_q;
+        const T e_b = okb ? ev[vb] : T(0);
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ra = wr + 16 * a + 4 * (lane >> 4) + r;
+                if (okb && ra < rows_p) {
+                    const T e_a = ev[p * kMp2Tile + ra];
+                    const T x = X[a][b][r];
+                    const T y = same ? x : Y[a][b][r];
+                    const T d_ab = (eij - e_a) - e_b;
+                    T term = (x * (T(2) * x - y)) / d_ab;
+                    sum += (double)term;
+                    if (mirror) {
+                        const T d_ba = (eij - e_b) - e_a;
+                        T term2 = (y * (T(2) * y - x)) / d_ba;
+                        sum += (double)term2;
+                    }
+                }
+            }
+        }
+    }
+    double blk = block256_sum(sum, red);
+    if (threadIdx.x == 0) {
+        if (!same) blk *= 2.0;
+        if (g.partial) g.partial[task] = blk;
+        else atomicAdd(g.accum, blk);
+    }
+}
+
+// Fixed-order sum of the per-workgroup partials (or the atomic accumulator)
+// into one element of T.
+template <typename T>
+__global__ __launch_bounds__(256) void mp2_finalize_kernel(const double* partial, int64_t n, T* out) {
+    __shared__ double red[4];
+    double s = 0.0;
+    for (int64_t k = threadIdx.x; k < n; k += 256) s += partial[k];
+    double tot = block256_sum(s, red);
+    if (threadIdx.x == 0) out[0] = (T)tot;
+}
+
+__global__ void zero_double_kernel(double* p) {
+    if (threadIdx.x == 0) p[0] = 0.0;
+}
+
+static int64_t mp2_ntasks(int64_t nocc, int64_t nvir) {
+    const int64_t nblk = (nvir + kMp2Tile - 1) / kMp2Tile;
+    return (nblk * (nblk + 1) / 2) * (nocc * (nocc + 1) / 2);
+}
+
+template <typename T>
+static int mp2_typed(int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eo, const void* ev,
+                     void* out, void* ws, int det, hipStream_t st) {
+    Mp2Args g;
+    g.B = B;
+    g.eo = eo;
+    g.ev = ev;
+    g.naux = naux;
+    g.nocc = (int)nocc;
+    g.nvir = (int)nvir;
+    g.nblk = (int)((nvir + kMp2Tile - 1) / kMp2Tile);
+    g.npq = (int64_t)g.nblk * (g.nblk + 1) / 2;
+    g.ntasks = mp2_ntasks(nocc, nvir);
+    double* w = static_cast<double*>(ws);
+    if (det) {
+        g.partial = w;
+        g.accum = nullptr;
+    } else {
+        g.partial = nullptr;
+        g.accum = w;
+        hipLaunchKernelGGL(zero_double_kernel, dim3(1), dim3(64), 0, st, w);
+    }
+    constexpr int V = Vec16<T>::n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && (naux % V == 0);
+    if (g.ntasks > 0) {
+        if (vec)
+            hipLaunchKernelGGL((mp2_energy_kernel<T, true>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+        else
+            hipLaunchKernelGGL((mp2_energy_kernel<T, false>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+    }
+    hipLaunchKernelGGL(mp2_finalize_kernel<T>, dim3(1), dim3(256), 0, st, (const double*)w,
+                       det ? g.ntasks : (int64_t)1, static_cast<T*>(out));
+    return check_launch("tt_mp2_energy");
+}
+
+}  // namespace tt
+
+extern "C" size_t tt_mp2_energy_workspace_bytes(int dtype, int64_t nocc, int64_t nvir, int64_t naux) {
+    (void)dtype;
+    (void)naux;
+    if (nocc < 0 || nvir < 0) return 0;
+    const size_t n = (size_t)tt::mp2_ntasks(nocc, nvir) + 1;
+    return ((n * sizeof(double) + 255) / 256) * 256;
+}
+
+extern "C" int tt_mp2_energy(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eps_occ,
+                             const void* eps_vir, void* energy_out, void* workspace, size_t workspace_bytes,
+                             int deterministic, void* stream) {
+    using namespace tt;
+    if (nocc < 0 || nvir < 0 || naux < 0)
+        return set_error(TT_INVALID, "tt_mp2_energy: negative extent (nocc=%lld nvir=%lld naux=%lld)",
+                         (long long)nocc, (long long)nvir, (long long)naux);
+    if (nocc > (1 << 20) || nvir > (1 << 24))
+        return set_error(TT_UNSUPPORTED, "tt_mp2_energy: nocc=%lld nvir=%lld beyond the kernel's index range",
+                         (long long)nocc, (long long)nvir);
+    if (mp2_ntasks(nocc, nvir) > 0x7fffffffLL)
+        return set_error(TT_UNSUPPORTED, "tt_mp2_energy: too many work units for one launch");
+    if (!energy_out || (nocc > 0 && nvir > 0 && (!B || !eps_occ || !eps_vir)))
+        return set_error(TT_INVALID, "tt_mp2_energy: NULL pointer");
+    const size_t need = tt_mp2_energy_workspace_bytes(dtype, nocc, nvir, naux);
+    if (!workspace || workspace_bytes < need)
+        return set_error(TT_INVALID, "tt_mp2_energy: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (dtype == TT_F64) return mp2_typed<double>(nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic, st);
+    if (dtype == TT_F32) return mp2_typed<float>(nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic, st);
+    return set_error(TT_UNSUPPORTED, "tt_mp2_energy: dtype %d (only TT_F32, TT_F64)", dtype);
+}

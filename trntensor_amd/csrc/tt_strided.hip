@@ -1,0 +1,235 @@
+// Strided multiply-reduce for contractions without a GEMM shape:
+//   D[o] = alpha * sum_r A[a_off(o) + a_roff(r)] * B[b_off(o) + b_roff(r)] (+ beta * C[o])
+//
+// Two schedules, chosen on the host:
+//  - one thread per output element (many outputs: outer products,
+//    permutations, small per-output reductions), grid-stride over outputs;
+//  - one workgroup per (output, reduction slice) (few outputs, long
+//    reductions: dots, traces, full contractions): 256 threads stride the
+//    slice, reduce with wavefront shuffles, and either finish the output or
+//    write a partial that a second kernel sums in a fixed order.
+// Multi-indices are decoded with precomputed fast-division multipliers; the
+// host splits any launch whose index range would reach 2^31.
+#include "tt_common.hpp"
+
+namespace tt {
+
+struct Dims {
+    int n;
+    FastDiv div[TT_MAX_DIMS];  // extents, innermost last
+    int64_t sa[TT_MAX_DIMS];
+    int64_t sb[TT_MAX_DIMS];
+};
+
+// Offsets of linear index `lin` (< 2^31) into A and B.
+__device__ __forceinline__ void decode(uint32_t lin, const Dims& d, int64_t& oa, int64_t& ob) {
+    oa = 0;
+    ob = 0;
+    for (int k = d.n - 1; k >= 0; --k) {
+        const uint32_t q = fdiv(lin, d.div[k]);
+        const uint32_t idx = lin - q * d.div[k].d;
+        oa += (int64_t)idx * d.sa[k];
+        ob += (int64_t)idx * d.sb[k];
+        lin = q;
+    }
+}
+
+struct StridedArgs {
+    const void* A;
+    const void* B;  // nullptr: factor 1
+    const void* C;  // nullptr: no beta term
+    void* D;
+    void* partial;  // nsplit * n_out elements of T, or nullptr
+    Dims out, red;
+    int64_t n_out;  // outputs in this launch (< 2^31)
+    int64_t n_red;  // reduction length (< 2^31)
+    int64_t nsplit;
+    double alpha, beta;
+};
+
+template <typename T>
+__device__ __forceinline__ T finish(const StridedArgs& g, int64_t o, T acc) {
+    T v = acc;
+    if (g.alpha != 1.0) v = (T)g.alpha * v;
+    if (g.C) v = v + (T)g.beta * static_cast<const T*>(g.C)[o];
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void strided_per_output_kernel(StridedArgs g) {
+    const T* A = static_cast<const T*>(g.A);
+    const T* B = static_cast<const T*>(g.B);
+    T* D = static_cast<T*>(g.D);
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < g.n_out; o += (int64_t)gridDim.x * 256) {
+        int64_t oa, ob;
+        decode((uint32_t)o, g.out, oa, ob);
+        T acc = T(0);
+        for (int64_t r = 0; r < g.n_red; ++r) {
+            int64_t ra, rb;
+            decode((uint32_t)r, g.red, ra, rb);
+            const T x = A[oa + ra];
+            acc += B ? x * B[ob + rb] : x;
+        }
+        D[o] = finish<T>(g, o, acc);
+    }
+}
+
+// Grid: (n_out, nsplit). Workgroup (o, s) reduces r = s*256 + t + k*nsplit*256.
+template <typename T>
+__global__ __launch_bounds__(256) void strided_per_block_kernel(StridedArgs g) {
+    __shared__ double red[4];
+    const T* A = static_cast<const T*>(g.A);
+    const T* B = static_cast<const T*>(g.B);
+    const int64_t o = blockIdx.x;
+    const int64_t s = blockIdx.y;
+    int64_t oa, ob;
+    decode((uint32_t)o, g.out, oa, ob);
+    T acc = T(0);
+    const int64_t step = g.nsplit * 256;
+    for (int64_t r = s * 256 + threadIdx.x; r < g.n_red; r += step) {
+        int64_t ra, rb;
+        decode((uint32_t)r, g.red, ra, rb);
+        const T x = A[oa + ra];
+        acc += B ? x * B[ob + rb] : x;
+    }
+    // Block sum in T: wavefront shuffles then four wave totals.
+    T v = acc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const T tot = ((T)red[0] + (T)red[1]) + ((T)red[2] + (T)red[3]);
+        if (g.nsplit == 1) static_cast<T*>(g.D)[o] = finish<T>(g, o, tot);
+        else static_cast<T*>(g.partial)[s * g.n_out + o] = tot;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void strided_finish_kernel(StridedArgs g) {
+    __shared__ double red[4];
+    const int64_t o = blockIdx.x;
+    const T* P = static_cast<const T*>(g.partial);
+    T acc = T(0);
+    for (int64_t s = threadIdx.x; s < g.nsplit; s += 256) acc += P[s * g.n_out + o];
+    T v = acc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const T tot = ((T)red[0] + (T)red[1]) + ((T)red[2] + (T)red[3]);
+        static_cast<T*>(g.D)[o] = finish<T>(g, o, tot);
+    }
+}
+
+// Host-side schedule choice shared by the workspace query and the launch.
+struct Plan {
+    bool per_block;
+    int64_t nsplit;
+};
+
+static Plan choose(int64_t n_out, int64_t n_red) {
+    Plan p{false, 1};
+    if (n_red > 1 && n_out < 8192) {
+        p.per_block = true;
+        // Enough workgroups to fill 256 CUs several times, each at least 2K elements.
+        int64_t want = (4096 + n_out - 1) / n_out;
+        int64_t cap = (n_red + 2047) / 2048;
+        p.nsplit = want < cap ? want : cap;
+        if (p.nsplit < 1) p.nsplit = 1;
+        if (p.nsplit > 65535) p.nsplit = 65535;
+    }
+    return p;
+}
+
+static int64_t prod(int n, const int64_t* s) {
+    int64_t r = 1;
+    for (int k = 0; k < n; ++k) r *= s[k];
+    return r;
+}
+
+template <typename T>
+static int run_typed(StridedArgs g, int n_out_dims, const int64_t* out_shape, hipStream_t st) {
+    const Plan pl = choose(g.n_out, g.n_red);
+    g.nsplit = pl.nsplit;
+    if (!pl.per_block) {
+        int64_t blocks = (g.n_out + 255) / 256;
+        if (blocks > 1 << 20) blocks = 1 << 20;
+        if (blocks > 0) hipLaunchKernelGGL(strided_per_output_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+    } else {
+        hipLaunchKernelGGL(strided_per_block_kernel<T>, dim3((unsigned)g.n_out, (unsigned)g.nsplit), dim3(256), 0, st, g);
+        if (g.nsplit > 1) hipLaunchKernelGGL(strided_finish_kernel<T>, dim3((unsigned)g.n_out), dim3(256), 0, st, g);
+    }
+    (void)n_out_dims;
+    (void)out_shape;
+    return check_launch("tt_strided_contract");
+}
+
+}  // namespace tt
+
+extern "C" size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, const int64_t* out_shape, int n_red,
+                                                      const int64_t* red_shape) {
+    using namespace tt;
+    if (n_out < 0 || n_red < 0 || n_out > TT_MAX_DIMS || n_red > TT_MAX_DIMS) return 0;
+    const int64_t no = prod(n_out, out_shape), nr = prod(n_red, red_shape);
+    const Plan p = choose(no, nr);
+    if (!p.per_block || p.nsplit == 1) return 0;
+    const size_t es = dtype == TT_F64 ? 8 : 4;
+    return ((size_t)(p.nsplit * no) * es + 255) / 256 * 256;
+}
+
+extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape, const int64_t* a_out_strides,
+                                   const int64_t* b_out_strides, int n_red, const int64_t* red_shape,
+                                   const int64_t* a_red_strides, const int64_t* b_red_strides, const void* A,
+                                   const void* B, double alpha, double beta, const void* C, void* D, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    using namespace tt;
+    if (n_out < 0 || n_red < 0 || n_out > TT_MAX_DIMS || n_red > TT_MAX_DIMS)
+        return set_error(TT_INVALID, "tt_strided_contract: dims out=%d red=%d (max %d)", n_out, n_red, TT_MAX_DIMS);
+    if (dtype != TT_F32 && dtype != TT_F64)
+        return set_error(TT_UNSUPPORTED, "tt_strided_contract: dtype %d (only TT_F32, TT_F64)", dtype);
+    for (int k = 0; k < n_out; ++k)
+        if (out_shape[k] < 0) return set_error(TT_INVALID, "tt_strided_contract: negative output extent");
+    for (int k = 0; k < n_red; ++k)
+        if (red_shape[k] < 0) return set_error(TT_INVALID, "tt_strided_contract: negative reduction extent");
+    const int64_t no = prod(n_out, out_shape), nr = prod(n_red, red_shape);
+    if (no == 0) return TT_OK;
+    if (!A || !D) return set_error(TT_INVALID, "tt_strided_contract: A or D is NULL");
+    if (no >= (1LL << 31) || nr >= (1LL << 31))
+        return set_error(TT_UNSUPPORTED, "tt_strided_contract: index range %lld x %lld reaches 2^31; split the call",
+                         (long long)no, (long long)nr);
+    const size_t need = tt_strided_contract_workspace_bytes(dtype, n_out, out_shape, n_red, red_shape);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return set_error(TT_INVALID, "tt_strided_contract: workspace of %zu bytes, need %zu", workspace_bytes, need);
+
+    StridedArgs g;
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.D = D;
+    g.partial = workspace;
+    g.n_out = no;
+    g.n_red = nr;
+    g.alpha = alpha;
+    g.beta = beta;
+    g.out.n = n_out;
+    for (int k = 0; k < n_out; ++k) {
+        g.out.div[k] = make_fastdiv((uint32_t)(out_shape[k] > 0 ? out_shape[k] : 1));
+        g.out.sa[k] = a_out_strides[k];
+        g.out.sb[k] = B ? b_out_strides[k] : 0;
+    }
+    g.red.n = n_red;
+    for (int k = 0; k < n_red; ++k) {
+        g.red.div[k] = make_fastdiv((uint32_t)(red_shape[k] > 0 ? red_shape[k] : 1));
+        g.red.sa[k] = a_red_strides[k];
+        g.red.sb[k] = B ? b_red_strides[k] : 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (nr == 0) {
+        // Empty reduction: every output is alpha * 0 (+ beta * C).
+        g.n_red = 0;
+    }
+    if (dtype == TT_F64) return run_typed<double>(g, n_out, out_shape, st);
+    return run_typed<float>(g, n_out, out_shape, st);
+}

@@ -1,0 +1,246 @@
+"""einsum front-end: dtype cast, planning, execution on the HIP kernels, and
+the alpha/beta epilogue fused into the last kernel's store.
+
+Mirrors trntensor/einsum.py (reference): same signature and keyword
+semantics (``alpha``, ``beta``, ``out``, ``dtype``, ``precision``), same
+error types, same path-executor step order. The results are what einsum
+defines; every step runs on libtrntensor_hip.so.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .hip import dispatch
+from .hip import engine
+from .plan import ContractionPlan, _parse_subscripts, plan_contraction
+
+_DTYPE_MAP: dict[str, torch.dtype] = {
+    "bf16": torch.bfloat16,
+    "bfloat16": torch.bfloat16,
+    "fp16": torch.float16,
+    "float16": torch.float16,
+    "f32": torch.float32,
+    "float32": torch.float32,
+    "f64": torch.float64,
+    "float64": torch.float64,
+}
+
+
+def _resolve_dtype(dtype: str | torch.dtype | None) -> torch.dtype | None:
+    """``None``, a ``torch.dtype``, or one of the strings above (case-insensitive);
+    anything else raises ``ValueError`` (reference trntensor/einsum.py:39-48)."""
+    if dtype is None or isinstance(dtype, torch.dtype):
+        return dtype
+    found = _DTYPE_MAP.get(dtype.lower())
+    if found is None:
+        raise ValueError(f"unknown dtype {dtype!r}; valid strings: {sorted(_DTYPE_MAP)}")
+    return found
+
+
+def einsum(
+    subscripts: str,
+    *operands: torch.Tensor,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    out: torch.Tensor | None = None,
+    dtype: str | torch.dtype | None = None,
+    precision: str = "fast",
+) -> torch.Tensor:
+    """Einstein summation with contraction planning, executed on MI355X.
+
+    Returns ``alpha * contract(operands) + beta * out`` (``out`` is read, never
+    written; the result is a new tensor, as in the reference). ``dtype`` casts
+    every operand first and the result comes back in that dtype.
+    ``precision="kahan"`` contracts in float64 and returns the first operand's
+    dtype; ``"dd"`` raises ``NotImplementedError``. The result lives on the
+    first operand's device: CPU operands are staged through the GPU.
+
+    Examples::
+
+        einsum("ij,jk->ik", A, B)
+        einsum("ij,jk->ik", A, B, alpha=2.0, beta=0.5, out=C)
+        einsum("ap,bp->ab", B[i], B[j])          # DF-MP2 pair block
+        einsum("mi,mnP->inP", C_occ, eri)        # AO->MO half transform
+        einsum("ia,jb,abP,ijP->", A, B, W, V)    # greedy path
+    """
+    target = _resolve_dtype(dtype)
+    if target is not None:
+        operands = tuple(op.to(target) for op in operands)
+    plan = plan_contraction(subscripts, *operands, precision=precision)
+    return _execute_contraction(subscripts, operands, plan, alpha=alpha, beta=beta, out=out)
+
+
+def _execute_contraction(
+    subscripts: str,
+    operands: tuple,
+    plan: ContractionPlan,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Run a plan (reference trntensor/einsum.py:106-126).
+
+    "kahan" contracts in float64 and casts back to the first operand's dtype;
+    "dd" raises. Otherwise the strategy selects the executor: matmul and bmm
+    go to the GEMM core, "torch" to the general engine, "path" to the
+    pairwise executor.
+    """
+    if plan.precision == "dd":
+        raise NotImplementedError(
+            "precision='dd' (double-double accumulation) has no kernel yet; "
+            "use precision='kahan' (fp64 accumulation) as an alternative."
+        )
+    dispatch.require_hip()
+    devs, orig = dispatch.place(*operands, *([out] if out is not None else []))
+    ops = devs[: len(operands)]
+    out_dev = devs[-1] if out is not None else None
+    dts = {o.dtype for o in ops}
+    if len(dts) > 1:
+        raise RuntimeError(f"einsum(): operands must share one dtype, got {sorted(str(d) for d in dts)}")
+    res_dtype = ops[0].dtype
+    cd = torch.float64 if plan.precision == "kahan" else dispatch.compute_dtype(res_dtype)
+    ops = [o.to(cd) for o in ops]
+    lhs, out_str = _parse_subscripts(subscripts)
+    terms = lhs.split(",")
+
+    C = None
+    if out_dev is not None:
+        shape = _result_shape(terms, out_str, ops)
+        C = out_dev.to(cd).expand(shape).contiguous()
+
+    if plan.strategy == "path":
+        res = _execute_path(terms, out_str, ops, plan.contraction_path, alpha, beta, C)
+    else:
+        res = engine.contract(
+            terms, out_str, ops, alpha, beta, C, prefer_gemm=plan.strategy in ("matmul", "bmm")
+        )
+    return res.to(res_dtype).to(orig)
+
+
+def _result_shape(terms, out_str, ops) -> list[int]:
+    ext: dict[str, int] = {}
+    for term, op in zip(terms, ops):
+        ext.update((c, int(n)) for c, n in zip(term, op.shape))
+    return [ext[c] for c in out_str]
+
+
+def _step_output(terms: list[str], i: int, j: int, out: str) -> str:
+    """Intermediate letters of a path step (reference trntensor/einsum.py:171-185):
+    free letters of terms[i] then terms[j] in first-seen order, minus letters
+    no later operand or the output needs."""
+    keep = set(out)
+    for k, term in enumerate(terms):
+        if k != i and k != j:
+            keep.update(term)
+    gone = (set(terms[i]) | set(terms[j])) - keep
+    seen: list[str] = []
+    for c in terms[i] + terms[j]:
+        if c not in gone and c not in seen:
+            seen.append(c)
+    return "".join(seen)
+
+
+def _path_names(terms: list[str], out: str, path: list[tuple[int, int]]) -> list[str]:
+    """Letter order of every intermediate.
+
+    Starts from the reference's naming. An intermediate's letter order is not
+    observable (only the final output's is), so when a step contracts two
+    tensors with the same letter set (a full or elementwise dot), the
+    operand produced earlier takes the other operand's order: the step then
+    streams both tensors contiguously instead of one of them transposed.
+    """
+    names: list[str] = []
+    cur = list(terms)
+    for s, (i, j) in enumerate(path):
+        name = out if s == len(path) - 1 else _step_output(cur, i, j, out)
+        names.append(name)
+        cur = [t for k, t in enumerate(cur) if k != i and k != j] + [name]
+
+    for _ in range(len(path)):
+        changed = False
+        cur = list(terms)
+        src: list[int | None] = [None] * len(terms)  # producing step of each entry
+        for s, (i, j) in enumerate(path):
+            ti, tj = cur[i], cur[j]
+            if (
+                len(set(ti)) == len(ti)
+                and len(set(tj)) == len(tj)
+                and set(ti) == set(tj)
+                and ti != tj
+            ):
+                pi, pj = src[i], src[j]
+                # rename the earlier-produced intermediate (never the final output)
+                cands = [(p, other) for p, other in ((pi, tj), (pj, ti)) if p is not None]
+                if cands:
+                    p, other = min(cands, key=lambda x: x[0])
+                    names[p] = other
+                    changed = True
+                    break
+            name = names[s]
+            cur = [t for k, t in enumerate(cur) if k != i and k != j] + [name]
+            src = [x for k, x in enumerate(src) if k != i and k != j] + [s]
+        if not changed:
+            break
+    return names
+
+
+def _execute_path(
+    terms: list[str],
+    out: str,
+    ops: list[torch.Tensor],
+    path: list[tuple[int, int]],
+    alpha: float,
+    beta: float,
+    C: torch.Tensor | None,
+) -> torch.Tensor:
+    """Pairwise execution of a greedy path (reference trntensor/einsum.py:151-193).
+
+    Each step contracts ``ops[i]`` and ``ops[j]`` on the HIP engine, removes
+    both and appends the result; the last step produces ``out`` and carries
+    the alpha/beta epilogue.
+    """
+    names = _path_names(terms, out, path)
+    cur_terms = list(terms)
+    cur = list(ops)
+    for s, (i, j) in enumerate(path):
+        last = s == len(path) - 1
+        res = engine.contract(
+            [cur_terms[i], cur_terms[j]],
+            names[s],
+            [cur[i], cur[j]],
+            alpha if last else 1.0,
+            beta if last else 0.0,
+            C if last else None,
+        )
+        cur = [t for k, t in enumerate(cur) if k != i and k != j] + [res]
+        cur_terms = [t for k, t in enumerate(cur_terms) if k != i and k != j] + [names[s]]
+    return cur[0]
+
+
+def multi_einsum(*contractions: tuple) -> list[torch.Tensor]:
+    """Several contractions in one call; each entry is ``(subscripts, *operands)``.
+
+    Operands that appear (by identity) in two or more contractions are copied
+    to the device once and reused; each result comes back on the device of
+    its contraction's first original operand (reference
+    trntensor/einsum.py:196-241).
+    """
+    counts: dict[int, int] = {}
+    keep: dict[int, torch.Tensor] = {}
+    for c in contractions:
+        for op in c[1:]:
+            counts[id(op)] = counts.get(id(op), 0) + 1
+            keep[id(op)] = op
+    pinned: dict[int, torch.Tensor] = {}
+    if dispatch.HAS_HIP and dispatch._use_hip():
+        pinned = {k: dispatch.to_device(keep[k]) for k, n in counts.items() if n > 1 and keep[k].device.type == "cpu"}
+    results = []
+    for c in contractions:
+        subs, originals = c[0], c[1:]
+        ops = tuple(pinned.get(id(op), op) for op in originals)
+        res = einsum(subs, *ops)
+        if originals and res.device != originals[0].device:
+            res = res.to(originals[0].device)
+        results.append(res)
+    return results

@@ -1,0 +1,252 @@
+"""HIP dispatch for the fused-contraction path: backend control, device
+placement, and the entry points that replace the reference's NKI dispatchers.
+
+Reference counterpart: trntensor/nki/dispatch.py. Differences by design:
+
+- Every contraction strategy executes on the HIP kernels; there is no FLOP
+  threshold (a HIP launch costs microseconds, not the NKI path's ~0.67 ms)
+  and no zero-padding (the kernels mask edge tiles).
+- There is no silent fallback to torch. A kernel error raises (ValueError /
+  NotImplementedError / RuntimeError by status code), which is what the
+  reference does under TRNTENSOR_REQUIRE_NKI=1; that variable and
+  TRNTENSOR_REQUIRE_HIP are accepted and change nothing. With no usable HIP
+  device, or with the "pytorch" backend selected, contraction calls raise
+  RuntimeError instead of computing on the host.
+- Residency: CPU operands are copied to the current HIP device, the kernels
+  run there, and the result is copied back to the first operand's device
+  (reference _to_xla / .to(orig), dispatch.py:127-149, 232). Operands already
+  on the device keep the result on the device.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib, engine
+
+# ---------------------------------------------------------------------------
+# availability and backend selection (reference dispatch.py:28-120)
+# ---------------------------------------------------------------------------
+_ARCH = "gfx950"
+
+
+def _probe() -> tuple[bool, str]:
+    if _lib.load() is None:
+        return False, _lib.load_error() or "library not loaded"
+    try:
+        if not torch.cuda.is_available():
+            return False, "no HIP device visible to torch"
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+    except Exception as exc:  # noqa: BLE001 - any runtime failure means unavailable
+        return False, f"HIP runtime error: {exc}"
+    if not arch.startswith(_ARCH):
+        return False, f"device arch {arch} is not {_ARCH}"
+    return True, ""
+
+
+HAS_HIP, _UNAVAILABLE_REASON = _probe()
+# Name kept for drop-in compatibility with code that tests trntensor.HAS_NKI.
+HAS_NKI = False
+
+_TRUTHY = ("1", "true", "yes")
+# Accepted for compatibility; errors always propagate in this build.
+_REQUIRE_HIP = os.environ.get("TRNTENSOR_REQUIRE_HIP", os.environ.get("TRNTENSOR_REQUIRE_NKI", "")).lower() in _TRUTHY
+
+_BACKENDS = ("auto", "pytorch", "hip", "nki")
+_backend = "auto"
+
+
+def set_backend(backend: str) -> None:
+    """Select "auto" (HIP when available), "hip" ("nki" is an alias), or "pytorch".
+
+    Unknown names raise AssertionError (the reference asserts, dispatch.py:96;
+    this check also survives ``python -O``). Selecting "hip" without a usable
+    gfx950 device raises RuntimeError and leaves the backend unchanged.
+    """
+    global _backend
+    if backend not in _BACKENDS:
+        raise AssertionError(f"backend must be one of {_BACKENDS}, got {backend!r}")
+    if backend in ("hip", "nki") and not HAS_HIP:
+        raise RuntimeError(f"HIP backend requires libtrntensor_hip and a {_ARCH} device: {_UNAVAILABLE_REASON}")
+    _backend = "hip" if backend == "nki" else backend
+
+
+def get_backend() -> str:
+    return _backend
+
+
+def _use_hip() -> bool:
+    """TRNTENSOR_FORCE_BACKEND > set_backend > availability (reference dispatch.py:108-120)."""
+    forced = os.environ.get("TRNTENSOR_FORCE_BACKEND", "").lower()
+    if forced in ("hip", "nki"):
+        return True
+    if forced == "pytorch":
+        return False
+    if _backend == "hip":
+        return True
+    if _backend == "pytorch":
+        return False
+    return HAS_HIP
+
+
+def require_hip() -> None:
+    """Raise unless contractions will run on the HIP kernels."""
+    if HAS_HIP and not _use_hip():
+        raise RuntimeError(
+            "trntensor_amd computes contractions only on its HIP kernels and the 'pytorch' "
+            "backend is selected; call torch.einsum directly for a host computation"
+        )
+    if not HAS_HIP:
+        raise RuntimeError(f"trntensor_amd HIP runtime unavailable: {_UNAVAILABLE_REASON}")
+
+
+# ---------------------------------------------------------------------------
+# residency (reference dispatch.py:127-184)
+# ---------------------------------------------------------------------------
+def _device() -> torch.device:
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_device(tensor: torch.Tensor) -> torch.Tensor:
+    """Move a tensor to the HIP device (no-op if already there).
+
+    Raises RuntimeError when no HIP runtime is available (reference
+    ``to_xla``, dispatch.py:152-177).
+    """
+    if tensor.device.type == "cuda":
+        return tensor
+    if not HAS_HIP:
+        raise RuntimeError(f"to_device requires the HIP runtime on a {_ARCH} device: {_UNAVAILABLE_REASON}")
+    return tensor.to(_device())
+
+
+def from_device(tensor: torch.Tensor) -> torch.Tensor:
+    """Move a tensor back to the CPU; no-op for CPU tensors."""
+    if tensor.device.type == "cpu":
+        return tensor
+    return tensor.to("cpu")
+
+
+# Drop-in names of the reference's residency helpers.
+to_xla = to_device
+from_xla = from_device
+
+
+def place(*tensors: torch.Tensor) -> tuple[list[torch.Tensor], torch.device]:
+    """Operands on one HIP device, plus the device the result goes back to."""
+    orig = tensors[0].device if tensors else _device()
+    cuda = [t.device for t in tensors if t.device.type == "cuda"]
+    dev = cuda[0] if cuda else _device()
+    if any(d != dev for d in cuda):
+        raise RuntimeError(f"operands on different devices: {sorted({str(d) for d in cuda})}")
+    return [t if t.device == dev else t.to(dev) for t in tensors], orig
+
+
+_WIDEN = {torch.bfloat16: torch.float32, torch.float16: torch.float32}
+
+
+def compute_dtype(dt: torch.dtype) -> torch.dtype:
+    """Kernel dtype for an operand dtype: fp32/fp64 as is, bf16/fp16 widened to fp32
+    (exact; products of 8/11-bit mantissas are exact in fp32 accumulation)."""
+    if dt in (torch.float32, torch.float64):
+        return dt
+    if dt in _WIDEN:
+        return _WIDEN[dt]
+    raise NotImplementedError(f"trntensor_amd HIP kernels do not compute in {dt}")
+
+
+# ---------------------------------------------------------------------------
+# entry points replacing the reference's NKI dispatchers
+# ---------------------------------------------------------------------------
+def hip_matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """2-D ``A @ B`` on the MFMA GEMM core (reference nki_matmul, dispatch.py:187-237)."""
+    return _binary("ij,jk->ik", A, B)
+
+
+def hip_batched_matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """``A[b] @ B[b]`` on the MFMA GEMM core (reference nki_batched_matmul, dispatch.py:339-387)."""
+    return _binary("bij,bjk->bik", A, B)
+
+
+def _binary(sub: str, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    require_hip()
+    lhs, out = sub.split("->")
+    (a, b), orig = place(A, B)
+    if a.dtype != b.dtype:
+        raise RuntimeError(f"expected both operands to have the same dtype, got {a.dtype} and {b.dtype}")
+    cd = compute_dtype(a.dtype)
+    res = engine.contract(lhs.split(","), out, [a.to(cd), b.to(cd)], prefer_gemm=True)
+    return res.to(a.dtype).to(orig)
+
+
+def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
+    """Fused DF-MP2 energy on tt_mp2_energy (reference _nki_mp2_energy, dispatch.py:240-283).
+
+    Returns a 0-D tensor of B's dtype on B's device.
+    """
+    require_hip()
+    lib = _lib.load()
+    (b, eo, ev), orig = place(B, eps_occ, eps_vir)
+    cd = compute_dtype(b.dtype)
+    b = b.to(cd).contiguous()
+    eo = eo.to(cd).contiguous()
+    ev = ev.to(cd).contiguous()
+    nocc, nvir, naux = b.shape
+    code = engine.dtype_code(cd)
+    wsb = lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux)
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=b.device)
+    e = torch.empty((), dtype=cd, device=b.device)
+    st = lib.tt_mp2_energy(
+        code,
+        nocc,
+        nvir,
+        naux,
+        engine._ptr(b),
+        engine._ptr(eo),
+        engine._ptr(ev),
+        engine._ptr(e),
+        engine._ptr(ws),
+        wsb,
+        int(bool(deterministic)),
+        engine._stream_ptr(b.device),
+    )
+    _lib.check(st, "tt_mp2_energy")
+    return e.to(B.dtype).to(orig)
+
+
+def _hip_ao_to_mo_transform(eri: torch.Tensor, C_occ: torch.Tensor, C_vir: torch.Tensor) -> torch.Tensor:
+    """Full AO->MO transform on tt_ao_to_mo_transform (reference
+    _nki_ao_to_mo_transform, dispatch.py:286-336). Result on eri's device."""
+    require_hip()
+    lib = _lib.load()
+    (e, co, cv), orig = place(eri, C_occ, C_vir)
+    if not (e.dtype == co.dtype == cv.dtype):
+        raise RuntimeError(f"expected one dtype, got {e.dtype}, {co.dtype}, {cv.dtype}")
+    cd = compute_dtype(e.dtype)
+    e = e.to(cd).contiguous()
+    co = co.to(cd).contiguous()
+    cv = cv.to(cd).contiguous()
+    nbasis, _, naux = e.shape
+    nocc, nvir = co.shape[1], cv.shape[1]
+    code = engine.dtype_code(cd)
+    wsb = lib.tt_ao_to_mo_workspace_bytes(code, nbasis, nocc, nvir, naux)
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=e.device)
+    out = torch.empty((nocc, nvir, naux), dtype=cd, device=e.device)
+    st = lib.tt_ao_to_mo_transform(
+        code,
+        nbasis,
+        nocc,
+        nvir,
+        naux,
+        engine._ptr(e),
+        engine._ptr(co),
+        engine._ptr(cv),
+        engine._ptr(out),
+        engine._ptr(ws),
+        wsb,
+        engine._stream_ptr(e.device),
+    )
+    _lib.check(st, "tt_ao_to_mo_transform")
+    return out.to(eri.dtype).to(orig)

@@ -1,0 +1,464 @@
+"""Contraction engine: maps any one- or two-operand einsum onto the HIP kernels.
+
+Every contraction on the path ends up in one of two kernels of
+libtrntensor_hip.so:
+
+- ``tt_gemm`` (MFMA core) when the contraction has a GEMM shape: letters
+  shared by both operands and the output form the batch, letters of one
+  operand and the output form M (of A) or N (of B), letters shared by both
+  operands but absent from the output form K. Each group must collapse to one
+  (extent, stride) pair in the operand and either K or the row group must be
+  unit-stride; otherwise the operand is first packed contiguously by
+  ``tt_strided_contract``. The output is written in place when its letter
+  order is batch+M+N (or batch+N+M, by swapping the operands), else through a
+  packed temporary and one permuting pass.
+- ``tt_strided_contract`` for everything without a GEMM shape: outer
+  products, elementwise products, traces, dots, permutations, letters summed
+  away, tiny matrix dimensions.
+
+The mapping is derived from letter positions and strides, never from the
+reference planner's strategy label, so index orders the reference's
+matmul/bmm executors mishandle (output order, summed free letters, bmm index
+positions; reference trntensor/plan.py:284-305) are computed as einsum
+defines them.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_MAX_INDEX = (1 << 31) - 1
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float64:
+        return _lib.TT_F64
+    if dt == torch.float32:
+        return _lib.TT_F32
+    raise NotImplementedError(f"HIP kernels compute in float32/float64, not {dt}")
+
+
+def _stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# letter bookkeeping
+# ---------------------------------------------------------------------------
+class Operand:
+    """A tensor view with one letter per dimension (no repeats)."""
+
+    __slots__ = ("t", "letters", "ext", "strd")
+
+    def __init__(self, term: str, t: torch.Tensor):
+        # Repeated letters select a diagonal: one dimension whose stride is the
+        # sum of the repeated dimensions' strides (a view, no data movement).
+        letters: list[str] = []
+        ext: list[int] = []
+        strd: list[int] = []
+        for c, n, s in zip(term, t.shape, t.stride()):
+            if c in letters:
+                strd[letters.index(c)] += s
+            else:
+                letters.append(c)
+                ext.append(int(n))
+                strd.append(int(s))
+        self.t = t
+        self.letters = letters
+        self.ext = dict(zip(letters, ext))
+        self.strd = dict(zip(letters, strd))
+
+
+def _merge(op: Operand, letters: list[str]) -> tuple[int, int] | None:
+    """Collapse `letters` (outer to inner) of `op` into one (extent, stride), or None."""
+    extent, stride = 1, 0
+    for c in reversed(letters):
+        n, s = op.ext[c], op.strd[c]
+        if n == 1:
+            continue
+        if extent == 1:
+            extent, stride = n, s
+        elif s == stride * extent:
+            extent *= n
+        else:
+            return None
+    return extent, stride
+
+
+def _numel(exts) -> int:
+    r = 1
+    for n in exts:
+        r *= int(n)
+    return r
+
+
+# ---------------------------------------------------------------------------
+# strided multiply-reduce
+# ---------------------------------------------------------------------------
+def _merge_dims(dims: list[tuple[int, int, int]]) -> list[tuple[int, int, int]]:
+    """Merge adjacent (extent, a_stride, b_stride) dims that are jointly contiguous;
+    drop extent-1 dims. Used for output dims (the output itself is row-major in
+    this order, so its strides always merge) and reduction dims."""
+    out: list[list[int]] = []
+    for n, sa, sb in dims:
+        if n == 1:
+            continue
+        if out:
+            pn, psa, psb = out[-1]
+            if psa == sa * n and psb == sb * n:
+                out[-1] = [pn * n, sa, sb]
+                continue
+        out.append([n, sa, sb])
+    return [tuple(d) for d in out]
+
+
+def strided_contract(
+    out_dims: list[tuple[int, int, int]],
+    red_dims: list[tuple[int, int, int]],
+    A: torch.Tensor,
+    B: torch.Tensor | None,
+    D: torch.Tensor,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+    a_off: int = 0,
+    b_off: int = 0,
+) -> None:
+    """D (contiguous, out_dims order) = alpha * sum_red A*B (+ beta*C), via tt_strided_contract.
+
+    Dims are (extent, stride in A, stride in B), element strides relative to
+    A/B's first element (``data_ptr()``) plus a_off/b_off. Launches are split so every index
+    range stays below 2^31.
+    """
+    lib = _lib.load()
+    out_dims = _merge_dims(out_dims)
+    red_dims = _merge_dims(red_dims)
+    n_out = _numel(d[0] for d in out_dims)
+    n_red = _numel(d[0] for d in red_dims)
+    if n_out == 0:
+        return
+    if len(out_dims) > _lib.TT_MAX_DIMS or len(red_dims) > _lib.TT_MAX_DIMS:
+        raise NotImplementedError("contraction with more than 8 independent strided dimensions")
+
+    # Split the outermost output dim while the output range reaches 2^31.
+    if n_out > _MAX_INDEX:
+        n0, sa0, sb0 = out_dims[0]
+        inner = n_out // n0
+        if inner > _MAX_INDEX:
+            raise NotImplementedError("output with more than 2^31 elements per outer index")
+        chunk = max(1, _MAX_INDEX // inner)
+        Dflat = D.view(-1)
+        Cflat = C.view(-1) if C is not None else None
+        for s in range(0, n0, chunk):
+            e = min(n0, s + chunk)
+            strided_contract(
+                [(e - s, sa0, sb0)] + out_dims[1:],
+                red_dims,
+                A,
+                B,
+                Dflat[s * inner : e * inner],
+                alpha,
+                beta,
+                None if Cflat is None else Cflat[s * inner : e * inner],
+                a_off + s * sa0,
+                b_off + s * sb0,
+            )
+        return
+    # Split the outermost reduction dim while the reduction range reaches 2^31;
+    # later chunks accumulate onto D (beta = 1, C = D).
+    if n_red > _MAX_INDEX:
+        n0, sa0, sb0 = red_dims[0]
+        inner = n_red // n0
+        if inner > _MAX_INDEX:
+            raise NotImplementedError("reduction with more than 2^31 elements per outer index")
+        chunk = max(1, _MAX_INDEX // inner)
+        first = True
+        for s in range(0, n0, chunk):
+            e = min(n0, s + chunk)
+            strided_contract(
+                out_dims,
+                [(e - s, sa0, sb0)] + red_dims[1:],
+                A,
+                B,
+                D,
+                alpha,
+                beta if first else 1.0,
+                C if first else D,
+                a_off + s * sa0,
+                b_off + s * sb0,
+            )
+            first = False
+        return
+
+    code = dtype_code(D.dtype)
+    es = D.element_size()
+    oshape = _lib.i64_array(d[0] for d in out_dims)
+    oa = _lib.i64_array(d[1] for d in out_dims)
+    ob = _lib.i64_array(d[2] for d in out_dims)
+    rshape = _lib.i64_array(d[0] for d in red_dims)
+    ra = _lib.i64_array(d[1] for d in red_dims)
+    rb = _lib.i64_array(d[2] for d in red_dims)
+    wsb = lib.tt_strided_contract_workspace_bytes(code, len(out_dims), oshape, len(red_dims), rshape)
+    ws = _workspace(wsb, D.device)
+    a_ptr = ctypes.c_void_p(A.data_ptr() + a_off * es)
+    b_ptr = None if B is None else ctypes.c_void_p(B.data_ptr() + b_off * es)
+    st = lib.tt_strided_contract(
+        code,
+        len(out_dims),
+        oshape,
+        oa,
+        ob,
+        len(red_dims),
+        rshape,
+        ra,
+        rb,
+        a_ptr,
+        b_ptr,
+        float(alpha),
+        float(beta),
+        _ptr(C),
+        _ptr(D),
+        _ptr(ws),
+        wsb,
+        _stream_ptr(D.device),
+    )
+    _lib.check(st, "tt_strided_contract")
+
+
+def pack(op: Operand, order: list[str]) -> torch.Tensor:
+    """Copy `op` into a new contiguous tensor with dims in `order`."""
+    D = torch.empty([op.ext[c] for c in order], dtype=op.t.dtype, device=op.t.device)
+    dims = [(op.ext[c], op.strd[c], 0) for c in order]
+    strided_contract(dims, [], op.t, None, D)
+    return D
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+def gemm(
+    transA: bool,
+    transB: bool,
+    M: int,
+    N: int,
+    K: int,
+    A: torch.Tensor,
+    lda: int,
+    sA: int,
+    B: torch.Tensor,
+    ldb: int,
+    sB: int,
+    D: torch.Tensor,
+    ldd: int,
+    sD: int,
+    batch: int = 1,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+    ldc: int = 0,
+    sC: int = 0,
+    a_off: int = 0,
+    b_off: int = 0,
+) -> None:
+    """tt_gemm on torch tensors (pointers taken at the given element offsets)."""
+    lib = _lib.load()
+    es = D.element_size()
+    st = lib.tt_gemm(
+        dtype_code(D.dtype),
+        int(transA),
+        int(transB),
+        M,
+        N,
+        K,
+        float(alpha),
+        ctypes.c_void_p(A.data_ptr() + a_off * es),
+        lda,
+        sA,
+        ctypes.c_void_p(B.data_ptr() + b_off * es),
+        ldb,
+        sB,
+        float(beta),
+        _ptr(C),
+        ldc,
+        sC,
+        _ptr(D),
+        ldd,
+        sD,
+        batch,
+        _stream_ptr(D.device),
+    )
+    _lib.check(st, "tt_gemm")
+
+
+def _gemm_layout(op: Operand, rows: list[str], ks: list[str]):
+    """(k_contiguous, ld) for an operand viewed as rows x K, or None."""
+    r = _merge(op, rows)
+    k = _merge(op, ks)
+    if r is None or k is None:
+        return None
+    (nr, sr), (nk, sk) = r, k
+    if nk == 1 or sk == 1:
+        ld = sr if nr > 1 else max(nk, 1)
+        if nr > 1 and ld < nk:
+            return None
+        return True, ld
+    if nr == 1 or sr == 1:
+        ld = sk
+        if ld < nr:
+            return None
+        return False, ld
+    return None
+
+
+def contract_gemm(
+    A: Operand,
+    B: Operand,
+    out: str,
+    batch: list[str],
+    ml: list[str],
+    nl: list[str],
+    kl: list[str],
+    alpha: float,
+    beta: float,
+    C: torch.Tensor | None,
+) -> torch.Tensor:
+    """Contraction with a GEMM shape through tt_gemm (operands packed only if needed)."""
+    dev, dt = A.t.device, A.t.dtype
+    ext = {**A.ext, **B.ext}
+    nb = _numel(ext[c] for c in batch)
+    M = _numel(ext[c] for c in ml)
+    N = _numel(ext[c] for c in nl)
+    K = _numel(ext[c] for c in kl)
+
+    la = _gemm_layout(A, ml, kl)
+    gba = _merge(A, batch)
+    if la is None or gba is None:
+        A = Operand("".join(batch + ml + kl), pack(A, batch + ml + kl))
+        la, gba = (True, max(K, 1)), (nb, M * K)
+    lb = _gemm_layout(B, nl, kl)
+    gbb = _merge(B, batch)
+    if lb is None or gbb is None:
+        B = Operand("".join(batch + kl + nl), pack(B, batch + kl + nl))
+        lb, gbb = (False, max(N, 1)), (nb, K * N)
+    sA = gba[1] if nb > 1 else 0
+    sB = gbb[1] if nb > 1 else 0
+
+    direct = "".join(batch + ml + nl) == out
+    swapped = (not direct) and "".join(batch + nl + ml) == out
+    shape = [ext[c] for c in out]
+    if direct or swapped:
+        D = torch.empty(shape, dtype=dt, device=dev)
+        Cc = None if C is None else C
+        if direct:
+            # A rows m: k-contiguous -> not transposed. B rows n: k-contiguous -> transposed.
+            gemm(not la[0], lb[0], M, N, K, A.t, la[1], sA, B.t, lb[1], sB, D, max(N, 1), M * N, nb,
+                 alpha, beta, Cc, max(N, 1), M * N)
+        else:
+            gemm(not lb[0], la[0], N, M, K, B.t, lb[1], sB, A.t, la[1], sA, D, max(M, 1), M * N, nb,
+                 alpha, beta, Cc, max(M, 1), M * N)
+        return D
+    # Packed [batch, M, N] temporary, then one permuting pass into the output order.
+    T = torch.empty([ext[c] for c in batch + ml + nl], dtype=dt, device=dev)
+    gemm(not la[0], lb[0], M, N, K, A.t, la[1], sA, B.t, lb[1], sB, T, max(N, 1), M * N, nb,
+         1.0, 0.0, None, 0, 0)
+    Top = Operand("".join(batch + ml + nl), T)
+    D = torch.empty(shape, dtype=dt, device=dev)
+    strided_contract([(Top.ext[c], Top.strd[c], 0) for c in out], [], T, None, D, alpha, beta, C)
+    return D
+
+
+# ---------------------------------------------------------------------------
+# public entry: one or two operands
+# ---------------------------------------------------------------------------
+def contract(
+    terms: list[str],
+    out: str,
+    tensors: list[torch.Tensor],
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+    prefer_gemm: bool = False,
+) -> torch.Tensor:
+    """einsum of one or two device tensors (same dtype, float32/float64).
+
+    C (if given) is contiguous in the output's shape and enters as beta*C.
+    """
+    ops = [Operand(t, x) for t, x in zip(terms, tensors)]
+    present = set().union(*[set(o.letters) for o in ops])
+    if len(set(out)) != len(out):
+        raise RuntimeError(f"einsum(): output subscript {out!r} includes a letter more than once")
+    missing = [c for c in out if c not in present]
+    if missing:
+        raise RuntimeError(f"einsum(): output subscript {missing[0]} does not appear in the equation for any input operand")
+    ext: dict[str, int] = {}
+    for o in ops:
+        ext.update(o.ext)
+    shape = [ext[c] for c in out]
+    dt, dev = tensors[0].dtype, tensors[0].device
+    dtype_code(dt)
+
+    if len(ops) == 2:
+        A, B = ops
+        la, lb, lo = set(A.letters), set(B.letters), set(out)
+        kl = [c for c in A.letters if c in lb and c not in lo]
+        batch = [c for c in out if c in la and c in lb]
+        ml = [c for c in out if c in la and c not in lb]
+        nl = [c for c in out if c in lb and c not in la]
+        if kl:
+            M = _numel(ext[c] for c in ml)
+            N = _numel(ext[c] for c in nl)
+            if prefer_gemm or (M >= 16 and N >= 16):
+                # Letters of one operand that are summed away are reduced first.
+                for idx, (op, other) in enumerate(((A, lb), (B, la))):
+                    gone = [c for c in op.letters if c not in other and c not in lo]
+                    if gone:
+                        keep = [c for c in op.letters if c not in gone]
+                        R = torch.empty([op.ext[c] for c in keep], dtype=dt, device=dev)
+                        strided_contract(
+                            [(op.ext[c], op.strd[c], 0) for c in keep],
+                            [(op.ext[c], op.strd[c], 0) for c in gone],
+                            op.t,
+                            None,
+                            R,
+                        )
+                        ops[idx] = Operand("".join(keep), R)
+                A, B = ops
+                # K letters ordered by A's strides (outer first) so A's K group collapses.
+                kl.sort(key=lambda c: -A.strd[c])
+                return contract_gemm(A, B, out, batch, ml, nl, kl, alpha, beta, C)
+
+    # Strided multiply-reduce over the whole contraction.
+    A = ops[0]
+    B = ops[1] if len(ops) == 2 else None
+
+    def s(op, c):
+        return 0 if op is None or c not in op.ext else op.strd[c]
+
+    red = [c for c in sorted(present - set(out))]
+    red.sort(key=lambda c: (-s(A, c), -s(B, c)))
+    D = torch.empty(shape, dtype=dt, device=dev)
+    strided_contract(
+        [(ext[c], s(A, c), s(B, c)) for c in out],
+        [(ext[c], s(A, c), s(B, c)) for c in red],
+        A.t,
+        None if B is None else B.t,
+        D,
+        alpha,
+        beta,
+        C,
+    )
+    return D
