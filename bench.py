@@ -1,0 +1,289 @@
+"""Benchmark of the fused-contraction hot path on one MI355X.
+
+Headline (BASELINE.json metric, config 4): DF-MP2 correlation energy,
+nocc=64 nvir=320 naux=1200, float64, inputs resident in HBM. One step = one
+trntensor_amd.mp2_energy call. value = algorithmic GFLOP/s
+(2080 occupied pairs i<=j x 2*nvir^2*naux = 5.112e11 FLOP per step).
+
+Also measured in the same run (secondary fields of the one JSON line):
+config 3 AO->MO half transform 'mi,mnP->inP' (GB/s and binding-roofline
+fraction), config 4 in float32, config 2 GEMM/bmm with alpha/beta, config 1
+einsum-loop latency, config 5 greedy path. The CPU baseline is the
+reference's CPU path restated in oracle/cpu_ref.py, timed on the host on a
+bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"f64": 78.6e12, "f32": 157.3e12, "hbm": 8.0e12}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5)")
+    return ap.parse_args()
+
+
+def timed(torch, fn, steps, warmup):
+    """(wall ms/step, mean event ms/step). Events are recorded on torch's
+    current stream, which is the stream the library launches on."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return wall, ev
+
+
+def mp2_inputs(torch, dtype, nocc=64, nvir=320, naux=1200):
+    g = torch.Generator().manual_seed(0)
+    B = torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64) * 0.05
+    eo = torch.sort(-20 + 19.7 * torch.rand(nocc, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(nvir, generator=g, dtype=torch.float64))[0]
+    return B.to(dtype), eo.to(dtype), ev.to(dtype)
+
+
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_mp2_baseline(torch, seconds=12.0):
+    """Reference CPU loop (oracle/cpu_ref.py, trntensor/quantum.py:87-100) on
+    config-4 fp64 inputs, over as many ordered (i, j) pairs as fit in about
+    `seconds`; scaled to the full 4096-pair job and reported in the GPU's unit
+    (algorithmic GFLOP/s over the i<=j work)."""
+    from oracle import cpu_ref
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    B, eo, ev = mp2_inputs(torch, torch.float64)
+    nocc = B.shape[0]
+    pairs = [(i, j) for i in range(nocc) for j in range(nocc)]
+    cpu_ref.mp2_energy_pairs(B, eo, ev, pairs[:4])  # warm-up
+    done, t0 = 0, time.perf_counter()
+    while done < len(pairs) and time.perf_counter() - t0 < seconds:
+        cpu_ref.mp2_energy_pairs(B, eo, ev, pairs[done : done + 64])
+        done += 64
+    dt = time.perf_counter() - t0
+    full = dt * len(pairs) / done
+    alg = 2080 * 2 * 320**2 * 1200
+    return {
+        "value": round(alg / full / 1e9, 2),
+        "unit": "GFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} of {len(pairs)} ordered (i,j) pairs of the reference loop in {dt:.1f} s, "
+        f"scaled to the full loop ({full:.1f} s); torch {torch.__version__} CPU",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path. "
+            "Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    import trntensor_amd as tt
+    from trntensor_amd.hip import dispatch
+
+    if not dispatch.HAS_HIP:
+        raise SystemExit(f"HIP path unavailable: {dispatch._UNAVAILABLE_REASON}")
+    dev = torch.device("cuda", 0)
+
+    # ---------------- headline: config 4, fp64 --------------------------------
+    B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, torch.float64))
+    flop = 2080 * 2 * 320**2 * 1200
+    print("bench: mp2_energy fp64 64x320x1200", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    wall, ev_ms = timed(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps, args.warmup)
+    value = flop / (wall * 1e-3) / 1e9
+    achieved = flop / (ev_ms * 1e-3)
+    line = {
+        "metric": "DF-MP2 energy GFLOP/s + % fp64 MFMA peak; AO->MO GB/s, 1 MI355X",
+        "value": round(value, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded torch.Generator, BASELINE config-4 distributions)",
+        "config": {
+            "workload": "mp2_energy fp64 nocc=64 nvir=320 naux=1200 (BASELINE config 4), inputs resident in HBM",
+            "global_batch": 1,
+            "flop_per_step": flop,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "mp2_energy_kernel<double>",
+            "achieved": round(achieved / 1e12, 2),
+            "peak": 78.6,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK["f64"], 4),
+            "traffic": traffic_from_profiles("mp2_energy_kernel<double>"),
+            "event_ms_per_launch": round(ev_ms, 4),
+        },
+    }
+    del B, eo, ev
+
+    extra = {}
+    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5"}
+    if not args.no_extra:
+        if "c3" in want:
+            extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
+            line["ao_to_mo_GBps"] = extra["c3_ao_to_mo_half_fp64"]["GB/s"]
+        if "c4f32" in want:
+            extra["c4_mp2_fp32"] = bench_c4_f32(torch, tt, dev, args)
+        if "c2" in want:
+            extra["c2"] = bench_c2(torch, tt, dev, args)
+        if "c1" in want:
+            extra["c1_einsum_loop_fp32"] = bench_c1(torch, tt, dev, args)
+        if "c5" in want:
+            extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
+        line["configs"] = extra
+
+    if not args.no_cpu:
+        print("bench: cpu baseline (reference loop sample)", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_mp2_baseline(torch)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def bench_c3(torch, tt, dev, args):
+    print("bench: c3 ao->mo half", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    C = torch.linalg.qr(torch.randn(512, 64, generator=g, dtype=torch.float64))[0].contiguous().to(dev)
+    eri = torch.randn(512, 512, 1536, generator=g, dtype=torch.float64).to(dev)
+    eri = ((eri + eri.permute(1, 0, 2)) * (0.05 / 2**0.5)).contiguous()
+    wall, ev_ms = timed(torch, lambda: tt.einsum("mi,mnP->inP", C, eri), max(5, args.steps), args.warmup)
+    byt = (512 * 512 * 1536 + 64 * 512 * 1536 + 512 * 64) * 8
+    flop = 2 * 64 * 512 * 512 * 1536
+    t = ev_ms * 1e-3
+    t_floor = max(flop / PEAK["f64"], byt / PEAK["hbm"])
+    return {
+        "ms": round(ev_ms, 4),
+        "wall_ms": round(wall, 4),
+        "GB/s": round(byt / t / 1e9, 1),
+        "TFLOP/s": round(flop / t / 1e12, 2),
+        "frac_hbm": round(byt / t / PEAK["hbm"], 4),
+        "frac_mfma": round(flop / t / PEAK["f64"], 4),
+        "frac_binding_roofline": round(t_floor / t, 4),
+        "bound": "mfma (AI 14.2 flop/B > fp64 ridge 9.8)",
+        "kernel": "gemm_kernel<double,64,256,TA,!TB>",
+    }
+
+
+def bench_c4_f32(torch, tt, dev, args):
+    print("bench: c4 mp2 fp32", file=sys.stderr, flush=True)
+    B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, torch.float32))
+    wall, ev_ms = timed(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps, args.warmup)
+    flop = 2080 * 2 * 320**2 * 1200
+    return {
+        "ms": round(ev_ms, 4),
+        "GFLOP/s": round(flop / (wall * 1e-3) / 1e9, 1),
+        "frac_mfma_f32": round(flop / (ev_ms * 1e-3) / PEAK["f32"], 4),
+    }
+
+
+def bench_c2(torch, tt, dev, args):
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    for name, shape, sub, flop in (
+        ("gemm4096", (4096, 4096), "ij,jk->ik", 2 * 4096**3),
+        ("bmm64x512", (64, 512, 512), "bij,bjk->bik", 64 * 2 * 512**3),
+    ):
+        for dt, key in ((torch.float64, "f64"), (torch.float32, "f32")):
+            print(f"bench: c2 {name} {key}", file=sys.stderr, flush=True)
+            A, B, C = (torch.randn(*shape, generator=g, dtype=torch.float64).to(dev, dt) for _ in range(3))
+            wall, ev_ms = timed(torch, lambda: tt.einsum(sub, A, B, alpha=1.5, beta=0.5, out=C), max(5, args.steps), args.warmup)
+            out[f"{name}_{key}"] = {
+                "ms": round(ev_ms, 4),
+                "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
+                "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK[key], 4),
+            }
+            del A, B, C
+    return out
+
+
+def bench_c1(torch, tt, dev, args):
+    """examples/df_mp2_einsum.py loop at config 1 with trntensor_amd.einsum per pair
+    (CPU operands, as in the config) and the fused call on the same CPU tensors."""
+    print("bench: c1 einsum loop", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    B = torch.randn(8, 32, 96, generator=g) * 0.1
+    eo = torch.sort(-20 + 19.7 * torch.rand(8, generator=g))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(32, generator=g))[0]
+
+    def loop():
+        e = 0.0
+        for i in range(8):
+            for j in range(8):
+                T = tt.einsum("ap,bp->ab", B[i], B[j])
+                d = eo[i] + eo[j] - ev.unsqueeze(1) - ev.unsqueeze(0)
+                e += (T * (2 * T - T.T) / d).sum().item()
+        return e
+
+    loop()
+    t0 = time.perf_counter()
+    loop()
+    t_loop = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(20):
+        float(tt.mp2_energy(B, eo, ev))
+    t_fused = (time.perf_counter() - t0) / 20
+    return {"einsum_loop_ms": round(t_loop * 1e3, 3), "fused_cpu_operands_ms": round(t_fused * 1e3, 3)}
+
+
+def bench_c5(torch, tt, dev, args):
+    print("bench: c5 greedy path", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    A = (torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1).to(dev)
+    B = (torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1).to(dev)
+    W = (torch.randn(400, 400, 800, generator=g, dtype=torch.float64) * 0.01).to(dev)
+    V = (torch.randn(128, 128, 800, generator=g, dtype=torch.float64) * 0.1).to(dev)
+    wall, ev_ms = timed(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V), 3, 1)
+    flop = 2.62144e9 + 2 * 2.097152e12 + 2 * 2.62144e9
+    return {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2), "path": "reference greedy [(0,1),(0,1),(0,1)]"}
+
+
+if __name__ == "__main__":
+    main()

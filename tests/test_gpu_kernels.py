@@ -88,7 +88,7 @@ def test_gemm_rejects_bad_arguments(hip):
         ("ii->", [(37, 37)]),
         ("ij->ji", [(33, 65)]),
         ("ijk->kj", [(5, 7, 9)]),
-        ("i,i->", [(100003,)]),
+        ("i,i->", [(100003,), (100003,)]),
         ("i,j->ij", [(130,), (70,)]),
         ("ij,ij->ij", [(40, 50), (40, 50)]),
         ("ij,jk->i", [(20, 30), (30, 10)]),

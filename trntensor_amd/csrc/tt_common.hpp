@@ -16,7 +16,9 @@ constexpr int kWave = 64;
 // MFMA 16x16x4 wrappers. One instruction computes a 16x16 block of
 // D += A(16x4) * B(4x16) across the 64 lanes of a wavefront:
 //   lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
-//   lane l holds D[4 * (l / 16) + r][l % 16] in accumulator element r.
+//   lane l holds D[row(l / 16, r)][l % 16] in accumulator element r, where
+//   row(g, r) = 4 g + r for f32 and g + 4 r for f64 (the f64 instruction
+//   interleaves its four 4-row groups across the accumulator registers).
 // ---------------------------------------------------------------------------
 typedef double d4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -31,6 +33,7 @@ struct Mfma<double> {
     static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
         return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
     }
+    static __device__ __forceinline__ int row(int g, int r) { return g + 4 * r; }
 };
 
 template <>
@@ -39,6 +42,7 @@ struct Mfma<float> {
     static __device__ __forceinline__ acc_t mma(float a, float b, acc_t c) {
         return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
     }
+    static __device__ __forceinline__ int row(int g, int r) { return 4 * g + r; }
 };
 
 // 16-byte vector of T (dwordx4 global/LDS access).

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
     T* D = static_cast<T*>(g.D) + bat * g.sD;
     const int col_l = lane & 15;
-    const int row_l = 4 * (lane >> 4);
+    const int lgrp = lane >> 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
             const int64_t col = n0 + wn0 + 16 * j + col_l;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = m0 + wm0 + 16 * i + row_l + r;
+                const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
                 if (row < g.M && col < g.N) {
                     T v = acc[i][j][r];
                     if (g.alpha != 1.0) v = alpha * v;

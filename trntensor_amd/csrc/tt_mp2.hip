@@ -230,7 +230,7 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ra = wr + 16 * a + 4 * (lane >> 4) + r;
+                const int ra = wr + 16 * a + MF::row(lane >> 4, r);
                 if (okb && ra < rows_p) {
                     const T e_a = ev[p * kMp2Tile + ra];
                     const T x = X[a][b][r];
