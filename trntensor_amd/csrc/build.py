@@ -34,6 +34,9 @@ HIPCC_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     "-munsafe-fp-atomics",
+    # keep MFMA accumulators in VGPRs (no per-iteration AGPR<->VGPR copies)
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
 ]

@@ -15,6 +15,8 @@
 // Inside a 16-wide stage, MFMA step s (0..3) gives lane-group g = lane / 16
 // the k index 4 g + s for both operands, so a lane's four k values are
 // adjacent in the [row][k] layout and one 32-byte read feeds four MFMAs.
+#include <type_traits>
+
 #include "tt_common.hpp"
 
 namespace tt {
@@ -61,29 +63,33 @@ struct Stage {
         }
     }
 
+    // FAST (interior stage: tile inside the matrix, 16-byte aligned): 
+    // unconditional vector loads. Otherwise element-wise loads from clamped
+    // addresses, zeroing what lies outside; no per-lane branches (which would
+    // serialise the prefetch behind waits).
+    template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
                                          int64_t k0, int64_t kdim) {
+        if (FAST) {
 #pragma unroll
-        for (int it = 0; it < PER_THREAD; ++it) {
-            int r, k;
-            place(it * kThreads + threadIdx.x, r, k);
-            const int64_t gr = row0 + r;
-            const int64_t gk = k0 + k;
-            if (KC) {
-                const T* src = p + gr * ld + gk;
-                if (VEC && gr < rows && gk + V <= kdim) {
-                    reg[it] = *reinterpret_cast<const vec_t*>(src);
-                } else {
+            for (int it = 0; it < PER_THREAD; ++it) {
+                int r, k;
+                place(it * kThreads + threadIdx.x, r, k);
+                const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
+                reg[it] = *reinterpret_cast<const vec_t*>(src);
+            }
+        } else {
 #pragma unroll
-                    for (int e = 0; e < V; ++e) reg[it][e] = (gr < rows && gk + e < kdim) ? src[e] : T(0);
-                }
-            } else {
-                const T* src = p + gk * ld + gr;
-                if (VEC && gk < kdim && gr + V <= rows) {
-                    reg[it] = *reinterpret_cast<const vec_t*>(src);
-                } else {
+            for (int it = 0; it < PER_THREAD; ++it) {
+                int r, k;
+                place(it * kThreads + threadIdx.x, r, k);
 #pragma unroll
-                    for (int e = 0; e < V; ++e) reg[it][e] = (gk < kdim && gr + e < rows) ? src[e] : T(0);
+                for (int e = 0; e < V; ++e) {
+                    const int64_t gr = row0 + r + (KC ? 0 : e);
+                    const int64_t gk = k0 + k + (KC ? e : 0);
+                    const bool ok = gr < rows && gk < kdim;
+                    const T x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
+                    reg[it][e] = ok ? x : T(0);
                 }
             }
         }
@@ -174,35 +180,53 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     SA sa;
     SB sb;
     const int64_t nk = (g.K + kBK - 1) / kBK;
-    if (nk > 0) {
-        sa.load(A, g.lda, m0, g.M, 0, g.K);
-        sb.load(B, g.ldb, n0, g.N, 0, g.K);
-        sa.store(bufA(0));
-        sb.store(bufB(0));
-    }
-    __syncthreads();
-
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            sa.load(A, g.lda, m0, g.M, (kt + 1) * kBK, g.K);
-            sb.load(B, g.ldb, n0, g.N, (kt + 1) * kBK, g.K);
-        }
+    // Stages 0 .. nfull-1 are interior for both operands.
+    const int64_t nfull = (VEC && m0 + BM <= g.M && n0 + BN <= g.N) ? g.K / kBK : 0;
+    auto load = [&](int64_t k0, auto fast) {
+        constexpr bool F = decltype(fast)::value;
+        sa.template load<F>(A, g.lda, m0, g.M, k0, g.K);
+        sb.template load<F>(B, g.ldb, n0, g.N, k0, g.K);
+    };
+    auto compute = [&](int buf) {
         T fa[4][4], fb[4][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) SA::frag(bufA(cur), wm0 + 16 * i, lane, fa[i]);
+        for (int i = 0; i < 4; ++i) SA::frag(bufA(buf), wm0 + 16 * i, lane, fa[i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) SB::frag(bufB(cur), wn0 + 16 * j, lane, fb[j]);
+        for (int j = 0; j < 4; ++j) SB::frag(bufB(buf), wn0 + 16 * j, lane, fb[j]);
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
+    };
+    if (nk > 0) {
+        if (nfull > 0) load(0, std::true_type{});
+        else load(0, std::false_type{});
+        sa.store(bufA(0));
+        sb.store(bufB(0));
+    }
+    __syncthreads();
+
+    // The scheduling barrier keeps the prefetch's LDS stores (and the wait for
+    // its global loads) behind this stage's MFMAs.
+    int64_t kt = 0;
+    for (; kt + 1 < nfull; ++kt) {
+        load((kt + 1) * kBK, std::true_type{});
+        compute(kt & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        sa.store(bufA((kt & 1) ^ 1));
+        sb.store(bufB((kt & 1) ^ 1));
+        __syncthreads();
+    }
+    for (; kt < nk; ++kt) {
+        const bool more = kt + 1 < nk;
+        if (more) load((kt + 1) * kBK, std::false_type{});
+        compute(kt & 1);
+        __builtin_amdgcn_sched_barrier(0);
         if (more) {
-            sa.store(bufA(cur ^ 1));
-            sb.store(bufB(cur ^ 1));
+            sa.store(bufA((kt & 1) ^ 1));
+            sb.store(bufB((kt & 1) ^ 1));
         }
         __syncthreads();
     }

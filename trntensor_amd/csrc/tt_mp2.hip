@@ -8,12 +8,13 @@
 // one workgroup forms
 //   X = B_i[p] B_j[q]^T    (T_ab for a in p, b in q)
 //   Y = B_j[p] B_i[q]^T    (T_ba at the same (a, b) position)
-// on MFMA in the same register layout, so the exchange term pairs X and Y
-// element by element with no transpose. For p < q the unit also accounts for
-// the mirrored block (q, p), whose terms are Y (2Y - X) / Delta_ba. For i = j,
-// Y equals X and is not recomputed. For i < j the unit's sum is doubled,
-// since the (j, i) pair contributes the same amount (Delta is symmetric).
-// T never leaves registers; each workgroup reduces to one double with
+// in the same register layout, so the exchange term pairs X and Y element by
+// element. Y comes from MFMA only for i < j, p < q; for p = q it is X^T
+// (one transpose through LDS), for i = j, p < q it is X itself. For p < q
+// the unit also accounts for the mirrored block (q, p), whose terms are
+// Y (2Y - X) / Delta_ba. For i < j the unit's sum is doubled, since the
+// (j, i) pair contributes the same amount (Delta is symmetric).
+// T never leaves registers and LDS; each workgroup reduces to one double with
 // wavefront shuffles and either stores it (deterministic mode, summed later
 // in a fixed order) or adds it with one atomic.
 //
@@ -21,6 +22,8 @@
 // (trntensor/quantum.py:97-99): denominator ((e_i + e_j) - e_a) - e_b with a
 // the row index, term (T * (2T - T^T)) / denominator with IEEE division, in
 // the input dtype; the energy is accumulated in double.
+#include <type_traits>
+
 #include "tt_common.hpp"
 
 namespace tt {
@@ -41,19 +44,32 @@ struct Panel {
 
     vec_t reg[PER_THREAD];
 
+    // FAST (interior stage: all 64 rows present, 16 k in range, 16-byte
+    // aligned): unconditional vector loads. Otherwise element-wise loads from
+    // clamped addresses, zeroing what lies outside; no per-lane branches.
+    template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
+        if (FAST) {
 #pragma unroll
-        for (int it = 0; it < PER_THREAD; ++it) {
-            const int v = it * kMp2Threads + threadIdx.x;
-            const int r = v / (kMp2BK / V);
-            const int k = (v % (kMp2BK / V)) * V;
-            const int64_t gk = k0 + k;
-            const T* src = base + (int64_t)r * naux + gk;
-            if (VEC && r < rows && gk + V <= naux) {
-                reg[it] = *reinterpret_cast<const vec_t*>(src);
-            } else {
+            for (int it = 0; it < PER_THREAD; ++it) {
+                const int v = it * kMp2Threads + threadIdx.x;
+                const int r = v / (kMp2BK / V);
+                const int k = (v % (kMp2BK / V)) * V;
+                reg[it] = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
+            }
+        } else {
 #pragma unroll
-                for (int e = 0; e < V; ++e) reg[it][e] = (r < rows && gk + e < naux) ? src[e] : T(0);
+            for (int it = 0; it < PER_THREAD; ++it) {
+                const int v = it * kMp2Threads + threadIdx.x;
+                const int r = v / (kMp2BK / V);
+                const int k = (v % (kMp2BK / V)) * V;
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const int64_t gk = k0 + k + e;
+                    const bool ok = r < rows && gk < naux;
+                    const T x = *(ok ? base + (int64_t)r * naux + gk : base);
+                    reg[it][e] = ok ? x : T(0);
+                }
             }
         }
     }
@@ -110,6 +126,101 @@ __device__ __forceinline__ void tri_decode(int64_t idx, int n, int& x, int& y) {
     y = r + (int)idx;
 }
 
+// K loop of one work unit: X = P0 Q0^T and, if NEED_Y, Y = P2 Q3^T, 16 k per
+// stage through double-buffered LDS. Stages whose successor is interior run
+// in the first loop with unconditional vector prefetch; the rest (edge rows,
+// the K remainder, the last stage) run in the second loop.
+template <typename T, bool VEC, bool NEED_Y>
+__device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* base1,
+                                          const T* base2, const T* base3, int rows_p, int rows_q, int64_t naux,
+                                          typename Mfma<T>::acc_t (&X)[2][2], typename Mfma<T>::acc_t (&Y)[2][2]) {
+    typedef Mfma<T> MF;
+    typedef Panel<T, VEC> PN;
+    // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS.
+    auto lds = [&](int b, int k) -> T* { return lds_base + (4 * b + k) * PN::ELEMS; };
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wr = (wave >> 1) * 32;
+    const int wc = (wave & 1) * 32;
+    const int64_t nk = (naux + kMp2BK - 1) / kMp2BK;
+    // Stages 0 .. nfull-1 are interior (all rows present, all 16 k in range).
+    const int64_t nfull = (VEC && rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / kMp2BK : 0;
+
+    PN s0, s1, s2, s3;
+    auto load = [&](int64_t k0, auto fast) {
+        constexpr bool F = decltype(fast)::value;
+        s0.template load<F>(base0, rows_p, naux, k0);
+        s1.template load<F>(base1, rows_q, naux, k0);
+        if (NEED_Y) {
+            s2.template load<F>(base2, rows_p, naux, k0);
+            s3.template load<F>(base3, rows_q, naux, k0);
+        }
+    };
+    auto store = [&](int buf) {
+        s0.store(lds(buf, 0));
+        s1.store(lds(buf, 1));
+        if (NEED_Y) {
+            s2.store(lds(buf, 2));
+            s3.store(lds(buf, 3));
+        }
+    };
+    auto compute = [&](int buf) {
+        T f0[2][4], f1[2][4];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) PN::frag(lds(buf, 0), wr + 16 * a, lane, f0[a]);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) PN::frag(lds(buf, 1), wc + 16 * b, lane, f1[b]);
+        if (NEED_Y) {
+            T f2[2][4], f3[2][4];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) PN::frag(lds(buf, 2), wr + 16 * a, lane, f2[a]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) PN::frag(lds(buf, 3), wc + 16 * b, lane, f3[b]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
+                        Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
+                    }
+        } else {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
+        }
+    };
+
+    if (nk == 0) return;
+    if (nfull > 0) load(0, std::true_type{});
+    else load(0, std::false_type{});
+    store(0);
+    __syncthreads();
+    int64_t kt = 0;
+    // The scheduling barrier keeps the prefetch's LDS stores (and the wait
+    // for its global loads) behind this stage's MFMAs, so load latency is
+    // covered by MFMA work instead of stalling the wave before it.
+    for (; kt + 1 < nfull; ++kt) {
+        load((kt + 1) * kMp2BK, std::true_type{});
+        compute(kt & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        store((kt & 1) ^ 1);
+        __syncthreads();
+    }
+    for (; kt < nk; ++kt) {
+        const bool more = kt + 1 < nk;
+        if (more) load((kt + 1) * kMp2BK, std::false_type{});
+        compute(kt & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) store((kt & 1) ^ 1);
+        __syncthreads();
+    }
+}
+
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     typedef Mfma<T> MF;
@@ -125,7 +236,8 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     int i, j, p, q;
     tri_decode(pair, g.nocc, i, j);
     tri_decode(u, g.nblk, p, q);
-    const bool same = (i == j);
+    // Y source: 0 = MFMA (i < j, p < q), 1 = X itself (i = j, p < q), 2 = X^T (p = q).
+    const int ymode = (p == q) ? 2 : (i == j ? 1 : 0);
 
     const T* B = static_cast<const T*>(g.B);
     const int64_t nvir = g.nvir;
@@ -151,67 +263,32 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
             Y[a][b] = acc_t{0, 0, 0, 0};
         }
 
-    PN s0, s1, s2, s3;
-    const int64_t nk = (g.naux + kMp2BK - 1) / kMp2BK;
-    s0.load(base0, rows_p, g.naux, 0);
-    s1.load(base1, rows_q, g.naux, 0);
-    if (!same) {
-        s2.load(base2, rows_p, g.naux, 0);
-        s3.load(base3, rows_q, g.naux, 0);
-    }
-    s0.store(lds[0][0]);
-    s1.store(lds[0][1]);
-    if (!same) {
-        s2.store(lds[0][2]);
-        s3.store(lds[0][3]);
-    }
-    __syncthreads();
+    if (ymode == 0)
+        mp2_kloop<T, VEC, true>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
+    else
+        mp2_kloop<T, VEC, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
 
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        const int64_t k1 = (kt + 1) * kMp2BK;
-        if (more) {
-            s0.load(base0, rows_p, g.naux, k1);
-            s1.load(base1, rows_q, g.naux, k1);
-            if (!same) {
-                s2.load(base2, rows_p, g.naux, k1);
-                s3.load(base3, rows_q, g.naux, k1);
-            }
-        }
-        T f0[2][4], f1[2][4];
+    const int lg = lane >> 4;
+    if (ymode == 2) {
+        // Y = X^T through LDS (the staging buffers are free after the last barrier).
+        constexpr int TP = kMp2Tile + 1;
+        T* tr = &lds[0][0][0];
+        static_assert(kMp2Tile * TP <= 2 * 4 * PN::ELEMS, "transpose fits in the staging buffers");
 #pragma unroll
-        for (int a = 0; a < 2; ++a) PN::frag(lds[cur][0], wr + 16 * a, lane, f0[a]);
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) PN::frag(lds[cur][1], wc + 16 * b, lane, f1[b]);
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
-        if (!same) {
-            T f2[2][4], f3[2][4];
-#pragma unroll
-            for (int a = 0; a < 2; ++a) PN::frag(lds[cur][2], wr + 16 * a, lane, f2[a]);
-#pragma unroll
-            for (int b = 0; b < 2; ++b) PN::frag(lds[cur][3], wc + 16 * b, lane, f3[b]);
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
-        }
-        if (more) {
-            s0.store(lds[cur ^ 1][0]);
-            s1.store(lds[cur ^ 1][1]);
-            if (!same) {
-                s2.store(lds[cur ^ 1][2]);
-                s3.store(lds[cur ^ 1][3]);
-            }
-        }
+                for (int r = 0; r < 4; ++r)
+                    tr[(wr + 16 * a + MF::row(lg, r)) * TP + wc + 16 * b + (lane & 15)] = X[a][b][r];
         __syncthreads();
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    Y[a][b][r] = tr[(wc + 16 * b + (lane & 15)) * TP + wr + 16 * a + MF::row(lg, r)];
     }
 
     // Epilogue: denominators and exchange term in registers.
@@ -230,11 +307,11 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ra = wr + 16 * a + MF::row(lane >> 4, r);
+                const int ra = wr + 16 * a + MF::row(lg, r);
                 if (okb && ra < rows_p) {
                     const T e_a = ev[p * kMp2Tile + ra];
                     const T x = X[a][b][r];
-                    const T y = same ? x : Y[a][b][r];
+                    const T y = ymode == 1 ? x : Y[a][b][r];
                     const T d_ab = (eij - e_a) - e_b;
                     T term = (x * (T(2) * x - y)) / d_ab;
                     sum += (double)term;
@@ -249,7 +326,7 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     }
     double blk = block256_sum(sum, red);
     if (threadIdx.x == 0) {
-        if (!same) blk *= 2.0;
+        if (i != j) blk *= 2.0;
         if (g.partial) g.partial[task] = blk;
         else atomicAdd(g.accum, blk);
     }
