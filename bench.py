@@ -38,6 +38,12 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5)")
+    ap.add_argument("--skip-headline", action="store_true", help="run only the extra configs")
+    ap.add_argument(
+        "--calibrate-copy",
+        action="store_true",
+        help="only copy 1 GiB device-to-device 5 times (reference kernel for the HBM byte counters)",
+    )
     return ap.parse_args()
 
 
@@ -124,6 +130,27 @@ def main():
     if not dispatch.HAS_HIP:
         raise SystemExit(f"HIP path unavailable: {dispatch._UNAVAILABLE_REASON}")
     dev = torch.device("cuda", 0)
+    if args.calibrate_copy:
+        x = torch.ones(1 << 27, dtype=torch.float64, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": x.numel() * 8, "bytes_written": y.numel() * 8, "launches": 5}))
+        return
+    if args.skip_headline:
+        extra = {}
+        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5"}
+        if "c3" in want:
+            extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
+        if "c4f32" in want:
+            extra["c4_mp2_fp32"] = bench_c4_f32(torch, tt, dev, args)
+        if "c2" in want:
+            extra["c2"] = bench_c2(torch, tt, dev, args)
+        if "c5" in want:
+            extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
+        print(json.dumps({"configs": extra}))
+        return
 
     # ---------------- headline: config 4, fp64 --------------------------------
     B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, torch.float64))
