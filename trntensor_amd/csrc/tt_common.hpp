@@ -59,6 +59,12 @@ struct Vec16<float> {
     static constexpr int n = 4;
 };
 
+// Vector of N values of T (N * sizeof(T) bytes).
+template <typename T, int N>
+struct VecN {
+    typedef T type __attribute__((ext_vector_type(N)));
+};
+
 // ---------------------------------------------------------------------------
 // Reductions
 // ---------------------------------------------------------------------------

@@ -39,70 +39,68 @@ struct GemmArgs {
 
 // One operand's ROWS x 16 stage: global -> registers -> LDS, plus fragment reads.
 // KC: element (row, k) at p[row * ld + k]; otherwise at p[k * ld + row].
+// Each thread stages E = ROWS / 16 elements that are contiguous in memory and
+// in LDS (one address per operand, NC 16-byte pieces at immediate offsets):
+//   KC: row t / (16 / E), k from (t % (16 / E)) E;   RC: k t / 16, rows from (t % 16) E.
 template <typename T, int ROWS, bool KC, bool VEC>
 struct Stage {
     static constexpr int V = Vec16<T>::n;
+    static constexpr int E = ROWS * kBK / kThreads;
+    static constexpr int NC = E / V;  // 16-byte pieces per thread
     static constexpr int PAD = 16 / sizeof(T);
     static constexpr int PITCH = KC ? (kBK + PAD) : (ROWS + PAD);
     static constexpr int ELEMS = KC ? ROWS * PITCH : kBK * PITCH;
-    static constexpr int NVEC = ROWS * kBK / V;
-    static constexpr int PER_THREAD = NVEC / kThreads;
-    static_assert(NVEC % kThreads == 0, "tile must split evenly over the workgroup");
+    static_assert(E % V == 0 && E <= kBK * (KC ? 1 : ROWS), "stage split");
     typedef typename Vec16<T>::type vec_t;
 
-    vec_t reg[PER_THREAD];
+    vec_t reg[NC];
 
-    // Position of vector `v` inside the tile.
-    __device__ __forceinline__ static void place(int v, int& row, int& k) {
+    __device__ __forceinline__ static void place(int& row, int& k) {
+        const int t = threadIdx.x;
         if (KC) {
-            row = v / (kBK / V);
-            k = (v % (kBK / V)) * V;
+            row = t / (kBK / E);
+            k = (t % (kBK / E)) * E;
         } else {
-            k = v / (ROWS / V);
-            row = (v % (ROWS / V)) * V;
+            k = t / (ROWS / E);
+            row = (t % (ROWS / E)) * E;
         }
     }
 
-    // FAST (interior stage: tile inside the matrix, 16-byte aligned): 
+    // FAST (interior stage: tile inside the matrix, 16-byte aligned):
     // unconditional vector loads. Otherwise element-wise loads from clamped
     // addresses, zeroing what lies outside; no per-lane branches (which would
     // serialise the prefetch behind waits).
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
                                          int64_t k0, int64_t kdim) {
+        int r, k;
+        place(r, k);
         if (FAST) {
+            const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
 #pragma unroll
-            for (int it = 0; it < PER_THREAD; ++it) {
-                int r, k;
-                place(it * kThreads + threadIdx.x, r, k);
-                const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
-                reg[it] = *reinterpret_cast<const vec_t*>(src);
-            }
+            for (int c = 0; c < NC; ++c) reg[c] = reinterpret_cast<const vec_t*>(src)[c];
         } else {
 #pragma unroll
-            for (int it = 0; it < PER_THREAD; ++it) {
-                int r, k;
-                place(it * kThreads + threadIdx.x, r, k);
+            for (int c = 0; c < NC; ++c) {
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
-                    const int64_t gr = row0 + r + (KC ? 0 : e);
-                    const int64_t gk = k0 + k + (KC ? e : 0);
+                    const int off = c * V + e;
+                    const int64_t gr = row0 + r + (KC ? 0 : off);
+                    const int64_t gk = k0 + k + (KC ? off : 0);
                     const bool ok = gr < rows && gk < kdim;
                     const T x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
-                    reg[it][e] = ok ? x : T(0);
+                    reg[c][e] = ok ? x : T(0);
                 }
             }
         }
     }
 
     __device__ __forceinline__ void store(T* s) const {
+        int r, k;
+        place(r, k);
+        vec_t* dst = reinterpret_cast<vec_t*>(KC ? (s + r * PITCH + k) : (s + k * PITCH + r));
 #pragma unroll
-        for (int it = 0; it < PER_THREAD; ++it) {
-            int r, k;
-            place(it * kThreads + threadIdx.x, r, k);
-            T* dst = KC ? (s + r * PITCH + k) : (s + k * PITCH + r);
-            *reinterpret_cast<vec_t*>(dst) = reg[it];
-        }
+        for (int c = 0; c < NC; ++c) dst[c] = reg[c];
     }
 
     // The four k values (MFMA steps 0..3) this lane feeds for the 16-row block at rb.
@@ -110,20 +108,10 @@ struct Stage {
         const int r = rb + (lane & 15);
         const int g = lane >> 4;
         if (KC) {
-            const vec_t* q = reinterpret_cast<const vec_t*>(s + r * PITCH + 4 * g);
-            if (V == 2) {
-                vec_t x0 = q[0], x1 = q[1];
-                out[0] = x0[0];
-                out[1] = x0[1];
-                out[2] = x1[0];
-                out[3] = x1[1];
-            } else {
-                vec_t x = q[0];
-                out[0] = x[0];
-                out[1] = x[1];
-                out[2] = x[2];
-                out[3] = x[3];
-            }
+            typedef typename VecN<T, 4>::type v4_t;
+            const v4_t x = *reinterpret_cast<const v4_t*>(s + r * PITCH + 4 * g);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) out[st] = x[st];
         } else {
 #pragma unroll
             for (int st = 0; st < 4; ++st) out[st] = s[(4 * g + st) * PITCH + r];
@@ -131,15 +119,17 @@ struct Stage {
     }
 };
 
-template <typename T, int BM, int BN, bool TA, bool TB, bool VEC>
+template <typename T, int BM, int BN, int FM, int FN, bool TA, bool TB, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
     typedef Stage<T, BM, !TA, VEC> SA;
     typedef Stage<T, BN, TB, VEC> SB;
-    constexpr int WAVES_N = BN / 64;
-    static_assert((BM / 64) * WAVES_N == 4, "four 64x64 wavefront tiles per workgroup");
+    // Each wavefront owns an (16 FM) x (16 FN) sub-tile: FM x FN MFMA blocks.
+    constexpr int WM = 16 * FM, WN = 16 * FN;
+    constexpr int WAVES_N = BN / WN;
+    static_assert((BM / WM) * WAVES_N == 4, "four wavefront tiles per workgroup");
 
     __shared__ __attribute__((aligned(16))) T lds[2 * (SA::ELEMS + SB::ELEMS)];
     // Stage buffers: A0 A1 B0 B1.
@@ -168,14 +158,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm0 = (wave / WAVES_N) * 64;
-    const int wn0 = (wave % WAVES_N) * 64;
+    const int wm0 = (wave / WAVES_N) * WM;
+    const int wn0 = (wave % WAVES_N) * WN;
 
-    acc_t acc[4][4];
+    acc_t acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+        for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
 
     SA sa;
     SB sb;
@@ -188,17 +178,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         sb.template load<F>(B, g.ldb, n0, g.N, k0, g.K);
     };
     auto compute = [&](int buf) {
-        T fa[4][4], fb[4][4];
+        T fa[FM][4], fb[FN][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) SA::frag(bufA(buf), wm0 + 16 * i, lane, fa[i]);
+        for (int i = 0; i < FM; ++i) SA::frag(bufA(buf), wm0 + 16 * i, lane, fa[i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) SB::frag(bufB(buf), wn0 + 16 * j, lane, fb[j]);
+        for (int j = 0; j < FN; ++j) SB::frag(bufB(buf), wn0 + 16 * j, lane, fb[j]);
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
+                for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
     };
     if (nk > 0) {
         if (nfull > 0) load(0, std::true_type{});
@@ -239,9 +229,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const int col_l = lane & 15;
     const int lgrp = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int64_t col = n0 + wn0 + 16 * j + col_l;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -257,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <typename T, int BM, int BN>
+template <typename T, int BM, int BN, int FM, int FN>
 static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) {
     g.tiles_m = (g.M + BM - 1) / BM;
     g.tiles_n = (g.N + BN - 1) / BN;
@@ -265,7 +255,7 @@ static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) 
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     dim3 grid((unsigned)total), block(kThreads);
 #define TT_GEMM_CASE(TA, TB, VC) \
-    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, TA, TB, VC>), grid, block, 0, st, g);
+    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, FM, FN, TA, TB, VC>), grid, block, 0, st, g);
     TT_GEMM_CASE(false, false, false)
     TT_GEMM_CASE(false, false, true)
     TT_GEMM_CASE(false, true, false)
@@ -285,9 +275,12 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 16-byte vectors need aligned bases, leading dimensions and batch strides.
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % V == 0 && g.ldb % V == 0;
     if (g.batch > 1) vec = vec && g.sA % V == 0 && g.sB % V == 0;
-    if (g.M <= 64) return launch_tile<T, 64, 256>(g, ta, tb, vec, st);
-    if (g.N <= 64) return launch_tile<T, 256, 64>(g, ta, tb, vec, st);
-    return launch_tile<T, 128, 128>(g, ta, tb, vec, st);
+    // Small-M (e.g. the AO->MO half transform, M = nocc): 64 x 128 tiles of
+    // four 32 x 64 wavefront tiles keep registers and LDS low enough for
+    // several workgroups per CU, i.e. more loads in flight on a long stream.
+    if (g.M <= 64) return launch_tile<T, 64, 128, 2, 4>(g, ta, tb, vec, st);
+    if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4>(g, ta, tb, vec, st);
+    return launch_tile<T, 128, 128, 4, 4>(g, ta, tb, vec, st);
 }
 
 int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {

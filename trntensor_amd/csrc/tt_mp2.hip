@@ -28,78 +28,56 @@
 
 namespace tt {
 
-constexpr int kMp2BK = 16;
 constexpr int kMp2Threads = 256;
 constexpr int kMp2Tile = 64;
+#ifndef TT_MP2_STAGE_K
+#define TT_MP2_STAGE_K 16
+#endif
+constexpr int kMp2StageK = TT_MP2_STAGE_K;  // k per LDS stage
 
-template <typename T, bool VEC>
+// One 64-row x BK stage of a B_i block, k contiguous in memory and in LDS
+// (row pitch BK + 16 bytes). Thread t stages row t / 4, elements
+// [(t % 4) E, (t % 4) E + E) with E = BK / 4: four consecutive threads read
+// one row's BK contiguous values. MFMA step s of a stage gives lane group
+// g = lane / 16 the k index E g + s, so a lane's E values per stage are
+// adjacent in LDS and one vector read feeds E MFMAs.
+template <typename T, int BK, bool VEC>
 struct Panel {
-    // 64 rows x 16 k of one B_i block, k contiguous in memory and in LDS.
-    static constexpr int V = Vec16<T>::n;
-    static constexpr int PITCH = kMp2BK + 16 / sizeof(T);
+    static constexpr int E = BK / 4;  // elements per thread, = MFMA steps per stage
+    static constexpr int PITCH = BK + 16 / sizeof(T);
     static constexpr int ELEMS = kMp2Tile * PITCH;
-    static constexpr int PER_THREAD = kMp2Tile * kMp2BK / V / kMp2Threads;
-    static_assert(PER_THREAD >= 1, "panel split");
-    typedef typename Vec16<T>::type vec_t;
+    static_assert(BK == 8 || BK == 16, "stage depth");
+    typedef typename VecN<T, E>::type vec_t;
 
-    vec_t reg[PER_THREAD];
+    vec_t reg;
 
-    // FAST (interior stage: all 64 rows present, 16 k in range, 16-byte
-    // aligned): unconditional vector loads. Otherwise element-wise loads from
-    // clamped addresses, zeroing what lies outside; no per-lane branches.
+    // FAST (interior stage: all 64 rows present, BK k in range, aligned):
+    // one unconditional vector load. Otherwise element-wise loads from clamped
+    // addresses, zeroing what lies outside; no per-lane branches.
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
+        const int r = threadIdx.x >> 2;
+        const int k = (threadIdx.x & 3) * E;
         if (FAST) {
-#pragma unroll
-            for (int it = 0; it < PER_THREAD; ++it) {
-                const int v = it * kMp2Threads + threadIdx.x;
-                const int r = v / (kMp2BK / V);
-                const int k = (v % (kMp2BK / V)) * V;
-                reg[it] = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
-            }
+            reg = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
         } else {
 #pragma unroll
-            for (int it = 0; it < PER_THREAD; ++it) {
-                const int v = it * kMp2Threads + threadIdx.x;
-                const int r = v / (kMp2BK / V);
-                const int k = (v % (kMp2BK / V)) * V;
-#pragma unroll
-                for (int e = 0; e < V; ++e) {
-                    const int64_t gk = k0 + k + e;
-                    const bool ok = r < rows && gk < naux;
-                    const T x = *(ok ? base + (int64_t)r * naux + gk : base);
-                    reg[it][e] = ok ? x : T(0);
-                }
+            for (int e = 0; e < E; ++e) {
+                const int64_t gk = k0 + k + e;
+                const bool ok = r < rows && gk < naux;
+                const T x = *(ok ? base + (int64_t)r * naux + gk : base);
+                reg[e] = ok ? x : T(0);
             }
         }
     }
 
     __device__ __forceinline__ void store(T* s) const {
-#pragma unroll
-        for (int it = 0; it < PER_THREAD; ++it) {
-            const int v = it * kMp2Threads + threadIdx.x;
-            const int r = v / (kMp2BK / V);
-            const int k = (v % (kMp2BK / V)) * V;
-            *reinterpret_cast<vec_t*>(s + r * PITCH + k) = reg[it];
-        }
+        *reinterpret_cast<vec_t*>(s + (threadIdx.x >> 2) * PITCH + (threadIdx.x & 3) * E) = reg;
     }
 
-    // Lane's four k values (MFMA steps 0..3: k = 4 g + step) for rows rb..rb+15.
-    __device__ __forceinline__ static void frag(const T* s, int rb, int lane, T out[4]) {
-        const vec_t* q = reinterpret_cast<const vec_t*>(s + (rb + (lane & 15)) * PITCH + 4 * (lane >> 4));
-        if (V == 2) {
-            vec_t x0 = q[0], x1 = q[1];
-            out[0] = x0[0];
-            out[1] = x0[1];
-            out[2] = x1[0];
-            out[3] = x1[1];
-        } else {
-            vec_t x = q[0];
-            out[0] = x[0];
-            out[1] = x[1];
-            out[2] = x[2];
-            out[3] = x[3];
-        }
+    // Lane's E k values (MFMA steps 0..E-1) for rows rb..rb+15.
+    __device__ __forceinline__ static vec_t frag(const T* s, int rb, int lane) {
+        return *reinterpret_cast<const vec_t*>(s + (rb + (lane & 15)) * PITCH + E * (lane >> 4));
     }
 };
 
@@ -126,25 +104,26 @@ __device__ __forceinline__ void tri_decode(int64_t idx, int n, int& x, int& y) {
     y = r + (int)idx;
 }
 
-// K loop of one work unit: X = P0 Q0^T and, if NEED_Y, Y = P2 Q3^T, 16 k per
-// stage through double-buffered LDS. Stages whose successor is interior run
-// in the first loop with unconditional vector prefetch; the rest (edge rows,
-// the K remainder, the last stage) run in the second loop.
-template <typename T, bool VEC, bool NEED_Y>
+// K loop of one work unit: X = P0 Q0^T and, if NEED_Y, Y = P2 Q3^T, BK k per
+// stage. Stages whose successor is interior run in the first loop with
+// unconditional vector prefetch; the rest (edge rows, the K remainder, the
+// last stage) run in the second loop.
+template <typename T, int BK, bool VEC, bool NEED_Y>
 __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* base1,
                                           const T* base2, const T* base3, int rows_p, int rows_q, int64_t naux,
                                           typename Mfma<T>::acc_t (&X)[2][2], typename Mfma<T>::acc_t (&Y)[2][2]) {
     typedef Mfma<T> MF;
-    typedef Panel<T, VEC> PN;
+    typedef Panel<T, BK, VEC> PN;
+    constexpr int KS = PN::E;
     // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS.
     auto lds = [&](int b, int k) -> T* { return lds_base + (4 * b + k) * PN::ELEMS; };
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wr = (wave >> 1) * 32;
     const int wc = (wave & 1) * 32;
-    const int64_t nk = (naux + kMp2BK - 1) / kMp2BK;
-    // Stages 0 .. nfull-1 are interior (all rows present, all 16 k in range).
-    const int64_t nfull = (VEC && rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / kMp2BK : 0;
+    const int64_t nk = (naux + BK - 1) / BK;
+    // Stages 0 .. nfull-1 are interior (all rows present, all BK k in range).
+    const int64_t nfull = (VEC && rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
 
     PN s0, s1, s2, s3;
     auto load = [&](int64_t k0, auto fast) {
@@ -165,19 +144,19 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
         }
     };
     auto compute = [&](int buf) {
-        T f0[2][4], f1[2][4];
+        typename PN::vec_t f0[2], f1[2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) PN::frag(lds(buf, 0), wr + 16 * a, lane, f0[a]);
+        for (int a = 0; a < 2; ++a) f0[a] = PN::frag(lds(buf, 0), wr + 16 * a, lane);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) PN::frag(lds(buf, 1), wc + 16 * b, lane, f1[b]);
+        for (int b = 0; b < 2; ++b) f1[b] = PN::frag(lds(buf, 1), wc + 16 * b, lane);
         if (NEED_Y) {
-            T f2[2][4], f3[2][4];
+            typename PN::vec_t f2[2], f3[2];
 #pragma unroll
-            for (int a = 0; a < 2; ++a) PN::frag(lds(buf, 2), wr + 16 * a, lane, f2[a]);
+            for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
 #pragma unroll
-            for (int b = 0; b < 2; ++b) PN::frag(lds(buf, 3), wc + 16 * b, lane, f3[b]);
+            for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
+            for (int st = 0; st < KS; ++st)
 #pragma unroll
                 for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -187,7 +166,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
                     }
         } else {
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
+            for (int st = 0; st < KS; ++st)
 #pragma unroll
                 for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -195,39 +174,43 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
         }
     };
 
+    // One LDS stage buffer and one register prefetch set: while stage k is
+    // multiplied out of LDS, stage k+1 is in flight in registers; after a
+    // barrier it replaces stage k. Half the LDS of double buffering buys a
+    // third workgroup per CU, whose MFMAs cover the extra barrier. The
+    // scheduling barrier keeps the wait for the prefetch behind the MFMAs.
     if (nk == 0) return;
     if (nfull > 0) load(0, std::true_type{});
     else load(0, std::false_type{});
     store(0);
     __syncthreads();
     int64_t kt = 0;
-    // The scheduling barrier keeps the prefetch's LDS stores (and the wait
-    // for its global loads) behind this stage's MFMAs, so load latency is
-    // covered by MFMA work instead of stalling the wave before it.
     for (; kt + 1 < nfull; ++kt) {
-        load((kt + 1) * kMp2BK, std::true_type{});
-        compute(kt & 1);
+        load((kt + 1) * BK, std::true_type{});
+        compute(0);
         __builtin_amdgcn_sched_barrier(0);
-        store((kt & 1) ^ 1);
+        __syncthreads();
+        store(0);
         __syncthreads();
     }
     for (; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
-        if (more) load((kt + 1) * kMp2BK, std::false_type{});
-        compute(kt & 1);
+        if (more) load((kt + 1) * BK, std::false_type{});
+        compute(0);
         __builtin_amdgcn_sched_barrier(0);
-        if (more) store((kt & 1) ^ 1);
+        __syncthreads();
+        if (more) store(0);
         __syncthreads();
     }
 }
 
-template <typename T, bool VEC>
+template <typename T, int BK, bool VEC>
 __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
-    typedef Panel<T, VEC> PN;
+    typedef Panel<T, BK, VEC> PN;
 
-    __shared__ __attribute__((aligned(16))) T lds[2][4][PN::ELEMS];
+    __shared__ __attribute__((aligned(16))) T lds[1][4][PN::ELEMS];
     __shared__ double red[4];
 
     const int64_t task = xcd_remap(blockIdx.x, g.ntasks);
@@ -264,16 +247,16 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
         }
 
     if (ymode == 0)
-        mp2_kloop<T, VEC, true>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
+        mp2_kloop<T, BK, VEC, true>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
     else
-        mp2_kloop<T, VEC, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
+        mp2_kloop<T, BK, VEC, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
 
     const int lg = lane >> 4;
     if (ymode == 2) {
         // Y = X^T through LDS (the staging buffers are free after the last barrier).
         constexpr int TP = kMp2Tile + 1;
         T* tr = &lds[0][0][0];
-        static_assert(kMp2Tile * TP <= 2 * 4 * PN::ELEMS, "transpose fits in the staging buffers");
+        static_assert(kMp2Tile * TP <= 4 * PN::ELEMS, "transpose fits in the staging buffers");
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -375,12 +358,13 @@ static int mp2_typed(int64_t nocc, int64_t nvir, int64_t naux, const void* B, co
         hipLaunchKernelGGL(zero_double_kernel, dim3(1), dim3(64), 0, st, w);
     }
     constexpr int V = Vec16<T>::n;
+    constexpr int BK = kMp2StageK;
     const bool vec = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && (naux % V == 0);
     if (g.ntasks > 0) {
         if (vec)
-            hipLaunchKernelGGL((mp2_energy_kernel<T, true>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, true>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
         else
-            hipLaunchKernelGGL((mp2_energy_kernel<T, false>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, false>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
     }
     hipLaunchKernelGGL(mp2_finalize_kernel<T>, dim3(1), dim3(256), 0, st, (const double*)w,
                        det ? g.ntasks : (int64_t)1, static_cast<T*>(out));
