@@ -179,6 +179,16 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // barrier it replaces stage k. Half the LDS of double buffering buys a
     // third workgroup per CU, whose MFMAs cover the extra barrier. The
     // scheduling barrier keeps the wait for the prefetch behind the MFMAs.
+    // fp64: the wave issuing its stage's MFMAs runs at raised priority, so
+    // co-resident waves in their load/store phase do not delay the MFMA
+    // stream (measured: +5 points of fp64 MFMA utilisation; fp32 loses, so
+    // it keeps the default priority).
+    auto prio_hi = [] {
+        if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
+    };
+    auto prio_lo = [] {
+        if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
+    };
     if (nk == 0) return;
     if (nfull > 0) load(0, std::true_type{});
     else load(0, std::false_type{});
@@ -187,7 +197,9 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     int64_t kt = 0;
     for (; kt + 1 < nfull; ++kt) {
         load((kt + 1) * BK, std::true_type{});
+        prio_hi();
         compute(0);
+        prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         store(0);
@@ -196,7 +208,9 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     for (; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
         if (more) load((kt + 1) * BK, std::false_type{});
+        prio_hi();
         compute(0);
+        prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         if (more) store(0);

@@ -304,6 +304,31 @@ def gemm(
     _lib.check(st, "tt_gemm")
 
 
+class _GemmRecipe:
+    """Launch parameters of a contraction that maps onto one tt_gemm call with
+    both operands in place; `swap` means the output is computed as B^T A^T."""
+
+    __slots__ = ("swap", "ta", "tb", "M", "N", "K", "lda", "sA", "ldb", "sB", "ldd", "sD", "batch", "shape", "dt")
+
+    def __init__(self, swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, batch, shape, dt):
+        self.swap, self.ta, self.tb = swap, ta, tb
+        self.M, self.N, self.K = M, N, K
+        self.lda, self.sA, self.ldb, self.sB, self.ldd, self.sD = lda, sA, ldb, sB, ldd, sD
+        self.batch, self.shape, self.dt = batch, shape, dt
+
+    def run(self, At, Bt, alpha, beta, C):
+        D = torch.empty(self.shape, dtype=self.dt, device=At.device)
+        X, Y = (Bt, At) if self.swap else (At, Bt)
+        gemm(self.ta, self.tb, self.M, self.N, self.K, X, self.lda, self.sA, Y, self.ldb, self.sB, D,
+             self.ldd, self.sD, self.batch, alpha, beta, C, self.ldd, self.sD)
+        return D
+
+
+# Recipes keyed by (terms, out, shapes, strides, dtype, prefer_gemm); bounded.
+_RECIPES: dict[tuple, _GemmRecipe] = {}
+_RECIPES_MAX = 4096
+
+
 def _gemm_layout(op: Operand, rows: list[str], ks: list[str]):
     """(k_contiguous, ld) for an operand viewed as rows x K, or None."""
     r = _merge(op, rows)
@@ -335,8 +360,13 @@ def contract_gemm(
     alpha: float,
     beta: float,
     C: torch.Tensor | None,
+    recipe_key: tuple | None = None,
 ) -> torch.Tensor:
-    """Contraction with a GEMM shape through tt_gemm (operands packed only if needed)."""
+    """Contraction with a GEMM shape through tt_gemm (operands packed only if needed).
+
+    When both operands are used in place and the output is written directly,
+    the launch parameters are cached under `recipe_key`.
+    """
     dev, dt = A.t.device, A.t.dtype
     ext = {**A.ext, **B.ext}
     nb = _numel(ext[c] for c in batch)
@@ -344,16 +374,19 @@ def contract_gemm(
     N = _numel(ext[c] for c in nl)
     K = _numel(ext[c] for c in kl)
 
+    packed = False
     la = _gemm_layout(A, ml, kl)
     gba = _merge(A, batch)
     if la is None or gba is None:
         A = Operand("".join(batch + ml + kl), pack(A, batch + ml + kl))
         la, gba = (True, max(K, 1)), (nb, M * K)
+        packed = True
     lb = _gemm_layout(B, nl, kl)
     gbb = _merge(B, batch)
     if lb is None or gbb is None:
         B = Operand("".join(batch + kl + nl), pack(B, batch + kl + nl))
         lb, gbb = (False, max(N, 1)), (nb, K * N)
+        packed = True
     sA = gba[1] if nb > 1 else 0
     sB = gbb[1] if nb > 1 else 0
 
@@ -361,16 +394,14 @@ def contract_gemm(
     swapped = (not direct) and "".join(batch + nl + ml) == out
     shape = [ext[c] for c in out]
     if direct or swapped:
-        D = torch.empty(shape, dtype=dt, device=dev)
-        Cc = None if C is None else C
         if direct:
             # A rows m: k-contiguous -> not transposed. B rows n: k-contiguous -> transposed.
-            gemm(not la[0], lb[0], M, N, K, A.t, la[1], sA, B.t, lb[1], sB, D, max(N, 1), M * N, nb,
-                 alpha, beta, Cc, max(N, 1), M * N)
+            rec = _GemmRecipe(0, not la[0], lb[0], M, N, K, la[1], sA, lb[1], sB, max(N, 1), M * N, nb, shape, dt)
         else:
-            gemm(not lb[0], la[0], N, M, K, B.t, lb[1], sB, A.t, la[1], sA, D, max(M, 1), M * N, nb,
-                 alpha, beta, Cc, max(M, 1), M * N)
-        return D
+            rec = _GemmRecipe(1, not lb[0], la[0], N, M, K, lb[1], sB, la[1], sA, max(M, 1), M * N, nb, shape, dt)
+        if recipe_key is not None and not packed:
+            _RECIPES[recipe_key] = rec
+        return rec.run(A.t, B.t, alpha, beta, C)
     # Packed [batch, M, N] temporary, then one permuting pass into the output order.
     T = torch.empty([ext[c] for c in batch + ml + nl], dtype=dt, device=dev)
     gemm(not la[0], lb[0], M, N, K, A.t, la[1], sA, B.t, lb[1], sB, T, max(N, 1), M * N, nb,
@@ -397,6 +428,15 @@ def contract(
 
     C (if given) is contiguous in the output's shape and enters as beta*C.
     """
+    key = None
+    if len(tensors) == 2:
+        a, b = tensors
+        key = (terms[0], terms[1], out, a.shape, a.stride(), b.shape, b.stride(), a.dtype, prefer_gemm)
+        rec = _RECIPES.get(key)
+        if rec is not None:
+            return rec.run(a, b, alpha, beta, C)
+        if len(_RECIPES) >= _RECIPES_MAX:
+            _RECIPES.clear()
     ops = [Operand(t, x) for t, x in zip(terms, tensors)]
     present = set().union(*[set(o.letters) for o in ops])
     if len(set(out)) != len(out):
@@ -439,7 +479,8 @@ def contract(
                 A, B = ops
                 # K letters ordered by A's strides (outer first) so A's K group collapses.
                 kl.sort(key=lambda c: -A.strd[c])
-                return contract_gemm(A, B, out, batch, ml, nl, kl, alpha, beta, C)
+                pre_reduced = A.t is not tensors[0] or B.t is not tensors[1]
+                return contract_gemm(A, B, out, batch, ml, nl, kl, alpha, beta, C, None if pre_reduced else key)
 
     # Strided multiply-reduce over the whole contraction.
     A = ops[0]
