@@ -188,3 +188,22 @@ def test_misplanned_detection():
     # the reference's own result differs from einsum semantics here
     res = cpu_ref.einsum("ij,jk->ki", torch.eye(3) * 2, torch.arange(9.0).view(3, 3))
     assert not torch.equal(res, torch.einsum("ij,jk->ki", torch.eye(3) * 2, torch.arange(9.0).view(3, 3)))
+
+
+def test_pairs_sampler_equals_full_loop():
+    """mp2_energy_pairs over every ordered pair is the reference loop itself."""
+    g = torch.Generator().manual_seed(8)
+    B = torch.randn(3, 6, 7, generator=g, dtype=torch.float64) * 0.1
+    eo = torch.sort(-20 + 19.7 * torch.rand(3, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(6, generator=g, dtype=torch.float64))[0]
+    pairs = [(i, j) for i in range(3) for j in range(3)]
+    assert torch.equal(cpu_ref.mp2_energy_pairs(B, eo, ev, pairs), cpu_ref.mp2_energy(B, eo, ev))
+
+
+def test_multi_einsum_is_a_loop_of_einsum():
+    g = torch.Generator().manual_seed(9)
+    A, B, C = (torch.randn(*s, generator=g, dtype=torch.float64) for s in [(4, 3), (3, 5), (5, 2)])
+    r = cpu_ref.multi_einsum(("ij,jk->ik", A, B), ("ij,jk,kl->il", A, B, C), ("ij,ij->", A, A))
+    np.testing.assert_allclose(r[0].numpy(), brute.einsum_f64("ij,jk->ik", A, B), rtol=1e-13)
+    np.testing.assert_allclose(r[1].numpy(), brute.einsum_f64("ij,jk,kl->il", A, B, C), rtol=1e-12)
+    np.testing.assert_allclose(float(r[2]), float(brute.einsum_f64("ij,ij->", A, A)), rtol=1e-13)
