@@ -68,6 +68,36 @@ int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
             void* D, int64_t ldd, int64_t strideD, int64_t batch, void* stream);
 
 /*
+ * Workspace (device bytes) that tt_gemm_dot needs.
+ */
+size_t tt_gemm_dot_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t batch);
+
+/*
+ * GEMM whose product is contracted on the spot instead of stored:
+ *   out[0] = alpha * sum_{b,m,n} (sum_k op(A)[m,k] op(B)[k,n]) * E(b,m,n)  (+ beta * C[0])
+ *   E(b,m,n) = E1[o(e1_strides)] * (E2 ? E2[o(e2_strides)] : 1),
+ *   o(s) = m_hi*s[0] + m_lo*s[1] + n_hi*s[2] + n_lo*s[3] + b*s[4],
+ *   (m_hi, m_lo) = divmod(m, m_lo_extent), (n_hi, n_lo) = divmod(n, n_lo_extent).
+ * op(A), op(B), batch strides as in tt_gemm. E1 alone is a tensor with the
+ * product's letters (any strides); E1 * E2 is an outer product of two factors
+ * that is never materialised. Each workgroup contributes one partial, summed
+ * in a fixed order. C (one element) is read iff non-NULL; out is one element.
+ *
+ * Replaces the last two steps of the reference's path executor when the final
+ * step is a full dot of a GEMM-shaped step's result
+ * (trntensor/einsum.py:151-193, each step a torch.einsum call at :188), e.g.
+ * the 'abP,ijP->abij' and 'iajb,abij->' steps of 'ia,jb,abP,ijP->'.
+ */
+int tt_gemm_dot(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
+                const void* A, int64_t lda, int64_t strideA,
+                const void* B, int64_t ldb, int64_t strideB, int64_t batch,
+                int64_t m_lo_extent, int64_t n_lo_extent,
+                const void* E1, const int64_t* e1_strides,
+                const void* E2, const int64_t* e2_strides,
+                double alpha, double beta, const void* C, void* out,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Workspace (device bytes) that tt_mp2_energy needs for this problem.
  */
 size_t tt_mp2_energy_workspace_bytes(int dtype, int64_t nocc, int64_t nvir, int64_t naux);

@@ -261,3 +261,46 @@ class TestConfig5:
         scale = torch.einsum("ijP,ijP->", torch.einsum("ibP,jb->ijP", torch.einsum("ia,abP->ibP", A.abs(), W.abs()), B.abs()), V.abs())
         assert abs(float(got) - float(ref)) / float(scale) <= 1e-14
         assert got.shape == () and got.dtype == torch.float64
+
+
+class TestPathFusion:
+    """A final full dot fused into the producing GEMM's epilogue (tt_gemm_dot):
+    results equal the reference's path executor (oracle) up to summation order,
+    bounded by the same contraction over absolute values."""
+
+    @staticmethod
+    def check(sub, shapes, dt=torch.float64, seed=0, **kw):
+        g = torch.Generator().manual_seed(seed)
+        ops = [torch.randn(*s, generator=g, dtype=torch.float64).to(dt) for s in shapes]
+        got = trntensor.einsum(sub, *[o.cuda() for o in ops], **kw)
+        ref = cpu_ref.einsum(sub, *[o.double() for o in ops], **kw)
+        scale = abs(float(torch.einsum(sub, *[o.double().abs() for o in ops]))) + abs(float(kw.get("out", torch.zeros(())))) + 1e-300
+        bar = 1e-14 if dt == torch.float64 else 1e-5
+        assert got.shape == () and got.dtype == dt
+        assert abs(float(got) - float(ref)) / scale <= bar, (float(got), float(ref))
+
+    def test_lazy_outer_product(self, hip):
+        self.check("ia,jb,abP,ijP->", [(6, 7), (5, 9), (7, 9, 11), (6, 5, 11)])
+
+    def test_lazy_outer_product_fp32(self, hip):
+        self.check("ia,jb,abP,ijP->", [(6, 7), (5, 9), (7, 9, 11), (6, 5, 11)], dt=torch.float32, seed=1)
+
+    def test_materialised_partner(self, hip):
+        self.check("ij,jk,ik->", [(70, 33), (33, 90), (70, 90)], seed=2)
+
+    def test_batch_letter(self, hip):
+        self.check("bij,bjk,bik->", [(3, 20, 17), (3, 17, 25), (3, 20, 25)], seed=3)
+
+    def test_alpha_beta_out(self, hip):
+        self.check("ij,jk,ik->", [(40, 30), (30, 50), (40, 50)], seed=4, alpha=1.5, beta=0.5, out=torch.tensor(2.0, dtype=torch.float64))
+
+    def test_unsupported_geometry_falls_back(self, hip):
+        # three letters in the M group: not decodable by the fused epilogue
+        self.check("abcK,Kde,abcde->", [(3, 4, 5, 6), (6, 7, 2), (3, 4, 5, 7, 2)], seed=5)
+
+    def test_plan_shape(self, hip):
+        from trntensor_amd.einsum import _fusion_plan, _path_names
+
+        path = [(0, 1), (0, 1), (0, 1)]
+        names = _path_names(["ia", "jb", "abP", "ijP"], "", path)
+        assert _fusion_plan(["ia", "jb", "abP", "ijP"], "", path, names) == (1, 0)

@@ -3,23 +3,11 @@
 #include <stdarg.h>
 #include <string.h>
 
-#include "tt_common.hpp"
+#include "tt_gemm.hpp"
 
 namespace tt {
 
-struct GemmArgs {
-    const void* A;
-    const void* B;
-    const void* C;
-    void* D;
-    int64_t M, N, K;
-    int64_t lda, ldb, ldc, ldd;
-    int64_t sA, sB, sC, sD;
-    int64_t batch;
-    int64_t tiles_m, tiles_n;
-    double alpha, beta;
-};
-int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
+
 
 static thread_local char g_err[512];
 

@@ -15,27 +15,16 @@
 // Inside a 16-wide stage, MFMA step s (0..3) gives lane-group g = lane / 16
 // the k index 4 g + s for both operands, so a lane's four k values are
 // adjacent in the [row][k] layout and one 32-byte read feeds four MFMAs.
+#include <string.h>
 #include <type_traits>
 
-#include "tt_common.hpp"
+#include "tt_gemm.hpp"
 
 namespace tt {
 
 constexpr int kBK = 16;
 constexpr int kThreads = 256;
 
-struct GemmArgs {
-    const void* A;
-    const void* B;
-    const void* C;
-    void* D;
-    int64_t M, N, K;
-    int64_t lda, ldb, ldc, ldd;
-    int64_t sA, sB, sC, sD;
-    int64_t batch;
-    int64_t tiles_m, tiles_n;
-    double alpha, beta;
-};
 
 // One operand's ROWS x 16 stage: global -> registers -> LDS, plus fragment reads.
 // KC: element (row, k) at p[row * ld + k]; otherwise at p[k * ld + row].
@@ -119,7 +108,7 @@ struct Stage {
     }
 };
 
-template <typename T, int BM, int BN, int FM, int FN, bool TA, bool TB, bool VEC>
+template <typename T, int BM, int BN, int FM, int FN, bool TA, bool TB, bool VEC, bool DOT>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
@@ -221,13 +210,46 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         __syncthreads();
     }
 
-    // Epilogue: D = alpha * acc (+ beta * C), masked at the matrix edge.
+    const int col_l = lane & 15;
+    const int lgrp = lane >> 4;
+    if (DOT) {
+        // Dot epilogue: sum of D .* E over this tile, one double per workgroup.
+        __shared__ double red[4];
+        const T* E1 = static_cast<const T*>(g.E1) + bat * g.e1s[4];
+        const T* E2 = g.E2 ? static_cast<const T*>(g.E2) + bat * g.e2s[4] : nullptr;
+        double sum = 0.0;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t col = n0 + wn0 + 16 * j + col_l;
+            const uint32_t nh = fdiv((uint32_t)col, g.ndiv);
+            const uint32_t nl = (uint32_t)col - nh * g.ndiv.d;
+            const int64_t o1n = nh * g.e1s[2] + nl * g.e1s[3];
+            const int64_t o2n = nh * g.e2s[2] + nl * g.e2s[3];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
+                    if (row < g.M && col < g.N) {
+                        const uint32_t mh = fdiv((uint32_t)row, g.mdiv);
+                        const uint32_t ml = (uint32_t)row - mh * g.mdiv.d;
+                        T e = E1[mh * g.e1s[0] + ml * g.e1s[1] + o1n];
+                        if (E2) e = e * E2[mh * g.e2s[0] + ml * g.e2s[1] + o2n];
+                        sum += (double)(acc[i][j][r] * e);
+                    }
+                }
+            }
+        }
+        const double tot = block256_sum(sum, red);
+        if (threadIdx.x == 0) g.partial[blockIdx.x] = tot;
+        return;
+    }
+
+    // Store epilogue: D = alpha * acc (+ beta * C), masked at the matrix edge.
     const T alpha = (T)g.alpha;
     const T beta = (T)g.beta;
     const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
     T* D = static_cast<T*>(g.D) + bat * g.sD;
-    const int col_l = lane & 15;
-    const int lgrp = lane >> 4;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -247,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <typename T, int BM, int BN, int FM, int FN>
+template <typename T, int BM, int BN, int FM, int FN, bool DOT>
 static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) {
     g.tiles_m = (g.M + BM - 1) / BM;
     g.tiles_n = (g.N + BN - 1) / BN;
@@ -255,7 +277,7 @@ static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) 
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     dim3 grid((unsigned)total), block(kThreads);
 #define TT_GEMM_CASE(TA, TB, VC) \
-    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, FM, FN, TA, TB, VC>), grid, block, 0, st, g);
+    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, FM, FN, TA, TB, VC, DOT>), grid, block, 0, st, g);
     TT_GEMM_CASE(false, false, false)
     TT_GEMM_CASE(false, false, true)
     TT_GEMM_CASE(false, true, false)
@@ -268,7 +290,7 @@ static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) 
     return check_launch("tt_gemm");
 }
 
-template <typename T>
+template <typename T, bool DOT>
 static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     constexpr int V = Vec16<T>::n;
     auto ok16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -278,15 +300,42 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // Small-M (e.g. the AO->MO half transform, M = nocc): 64 x 128 tiles of
     // four 32 x 64 wavefront tiles keep registers and LDS low enough for
     // several workgroups per CU, i.e. more loads in flight on a long stream.
-    if (g.M <= 64) return launch_tile<T, 64, 128, 2, 4>(g, ta, tb, vec, st);
-    if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4>(g, ta, tb, vec, st);
-    return launch_tile<T, 128, 128, 4, 4>(g, ta, tb, vec, st);
+    if (g.M <= 64) return launch_tile<T, 64, 128, 2, 4, DOT>(g, ta, tb, vec, st);
+    if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4, DOT>(g, ta, tb, vec, st);
+    return launch_tile<T, 128, 128, 4, 4, DOT>(g, ta, tb, vec, st);
 }
 
 int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
-    if (dtype == TT_F64) return gemm_typed<double>(g, ta, tb, st);
-    if (dtype == TT_F32) return gemm_typed<float>(g, ta, tb, st);
+    g.E1 = g.E2 = nullptr;
+    g.partial = nullptr;
+    if (dtype == TT_F64) return gemm_typed<double, false>(g, ta, tb, st);
+    if (dtype == TT_F32) return gemm_typed<float, false>(g, ta, tb, st);
     return set_error(TT_UNSUPPORTED, "tt_gemm: dtype %d (only TT_F32, TT_F64)", dtype);
+}
+
+int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts) {
+    int rc;
+    if (dtype == TT_F64) rc = gemm_typed<double, true>(g, ta, tb, st);
+    else if (dtype == TT_F32) rc = gemm_typed<float, true>(g, ta, tb, st);
+    else return set_error(TT_UNSUPPORTED, "tt_gemm_dot: dtype %d (only TT_F32, TT_F64)", dtype);
+    *nparts = g.tiles_m * g.tiles_n * g.batch;
+    return rc;
+}
+
+// out[0] = alpha * (fixed-order sum of the partials) (+ beta * C[0]).
+template <typename T>
+__global__ __launch_bounds__(256) void dot_finalize_kernel(const double* partial, int64_t n, double alpha, double beta,
+                                                           const T* C, T* out) {
+    __shared__ double red[4];
+    double s = 0.0;
+    for (int64_t k = threadIdx.x; k < n; k += 256) s += partial[k];
+    const double tot = block256_sum(s, red);
+    if (threadIdx.x == 0) {
+        T v = (T)tot;
+        if (alpha != 1.0) v = (T)alpha * v;
+        if (C) v = v + (T)beta * C[0];
+        out[0] = v;
+    }
 }
 
 }  // namespace tt
@@ -329,4 +378,74 @@ extern "C" int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, 
     g.alpha = alpha;
     g.beta = beta;
     return gemm_dispatch(dtype, transA != 0, transB != 0, g, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t tt_gemm_dot_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t batch) {
+    (void)dtype;
+    if (M <= 0 || N <= 0 || batch <= 0) return 256;
+    // One double per workgroup; every tile configuration is at least 64 x 64.
+    const size_t parts = (size_t)((M + 63) / 64) * (size_t)((N + 63) / 64) * (size_t)batch;
+    return ((parts * sizeof(double) + 255) / 256) * 256;
+}
+
+extern "C" int tt_gemm_dot(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K, const void* A,
+                           int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, int64_t batch,
+                           int64_t m_lo, int64_t n_lo, const void* E1, const int64_t* e1_strides, const void* E2,
+                           const int64_t* e2_strides, double alpha, double beta, const void* C, void* out,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace tt;
+    if (M < 0 || N < 0 || K < 0 || batch < 0)
+        return set_error(TT_INVALID, "tt_gemm_dot: negative extent (M=%lld N=%lld K=%lld batch=%lld)", (long long)M,
+                         (long long)N, (long long)K, (long long)batch);
+    if (dtype != TT_F32 && dtype != TT_F64)
+        return set_error(TT_UNSUPPORTED, "tt_gemm_dot: dtype %d (only TT_F32, TT_F64)", dtype);
+    if (!out || !workspace) return set_error(TT_INVALID, "tt_gemm_dot: out or workspace is NULL");
+    if (M >= (1LL << 31) || N >= (1LL << 31))
+        return set_error(TT_UNSUPPORTED, "tt_gemm_dot: M or N reaches 2^31");
+    const int64_t mlo = m_lo > 0 ? m_lo : 1, nlo = n_lo > 0 ? n_lo : 1;
+    const size_t need = tt_gemm_dot_workspace_bytes(dtype, M, N, batch);
+    if (workspace_bytes < need)
+        return set_error(TT_INVALID, "tt_gemm_dot: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int64_t nparts = 0;
+    if (M > 0 && N > 0 && batch > 0) {
+        if (K > 0 && (!A || !B)) return set_error(TT_INVALID, "tt_gemm_dot: A or B is NULL");
+        if (!E1 || !e1_strides || (E2 && !e2_strides)) return set_error(TT_INVALID, "tt_gemm_dot: E1 is NULL");
+        const int64_t rowsA = transA ? K : M, colsA = transA ? M : K;
+        const int64_t rowsB = transB ? N : K, colsB = transB ? K : N;
+        if (K > 0 && ((rowsA > 1 && lda < colsA) || (rowsB > 1 && ldb < colsB)))
+            return set_error(TT_INVALID, "tt_gemm_dot: leading dimension smaller than a row (lda=%lld ldb=%lld)",
+                             (long long)lda, (long long)ldb);
+        GemmArgs g;
+        memset(&g, 0, sizeof(g));
+        g.A = A;
+        g.B = B;
+        g.M = M;
+        g.N = N;
+        g.K = K;
+        g.lda = lda;
+        g.ldb = ldb;
+        g.sA = strideA;
+        g.sB = strideB;
+        g.batch = batch;
+        g.alpha = 1.0;
+        g.E1 = E1;
+        g.E2 = E2;
+        for (int k = 0; k < 5; ++k) {
+            g.e1s[k] = e1_strides[k];
+            g.e2s[k] = E2 ? e2_strides[k] : 0;
+        }
+        g.mdiv = make_fastdiv((uint32_t)mlo);
+        g.ndiv = make_fastdiv((uint32_t)nlo);
+        g.partial = static_cast<double*>(workspace);
+        const int rc = gemm_dot_dispatch(dtype, transA != 0, transB != 0, g, st, &nparts);
+        if (rc != TT_OK) return rc;
+    }
+    if (dtype == TT_F64)
+        hipLaunchKernelGGL(dot_finalize_kernel<double>, dim3(1), dim3(256), 0, st, (const double*)workspace, nparts,
+                           alpha, beta, static_cast<const double*>(C), static_cast<double*>(out));
+    else
+        hipLaunchKernelGGL(dot_finalize_kernel<float>, dim3(1), dim3(256), 0, st, (const double*)workspace, nparts,
+                           alpha, beta, static_cast<const float*>(C), static_cast<float*>(out));
+    return check_launch("tt_gemm_dot");
 }

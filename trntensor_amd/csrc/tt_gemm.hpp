@@ -1,0 +1,37 @@
+// Host-side interface of the MFMA GEMM core shared by the C-ABI sources.
+#pragma once
+
+#include "tt_common.hpp"
+
+namespace tt {
+
+struct GemmArgs {
+    const void* A;
+    const void* B;
+    const void* C;
+    void* D;
+    int64_t M, N, K;
+    int64_t lda, ldb, ldc, ldd;
+    int64_t sA, sB, sC, sD;
+    int64_t batch;
+    int64_t tiles_m, tiles_n;
+    double alpha, beta;
+    // Dot epilogue: instead of storing D, each workgroup writes
+    // sum_{m,n} D[m,n] * E(m,n) to partial[workgroup], with
+    // E(m,n) = E1[off1] * (E2 ? E2[off2] : 1), off = m_hi*s[0] + m_lo*s[1] +
+    // n_hi*s[2] + n_lo*s[3] + batch*s[4], (m_hi, m_lo) = divmod(m, mdiv.d),
+    // (n_hi, n_lo) = divmod(n, ndiv.d).
+    const void* E1;
+    const void* E2;
+    int64_t e1s[5], e2s[5];
+    FastDiv mdiv, ndiv;
+    double* partial;
+};
+
+// tt_gemm after argument checks (store epilogue).
+int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
+// Dot epilogue; writes one double per workgroup to g.partial and returns the
+// number of workgroups in *nparts.
+int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);
+
+}  // namespace tt

@@ -185,6 +185,43 @@ def _path_names(terms: list[str], out: str, path: list[tuple[int, int]]) -> list
     return names
 
 
+def _fusion_plan(terms: list[str], out: str, path: list[tuple[int, int]], names: list[str]):
+    """Steps whose results are never materialised, or None.
+
+    When the path ends in a full dot (scalar output) of two tensors with the
+    same letters and one of them is produced by a GEMM-shaped step, that
+    step's product is contracted in the GEMM epilogue instead of stored. If
+    the dot's other operand is produced by an outer-product step (no shared
+    letters), it stays unevaluated too: its two factors multiply in the same
+    epilogue. Returns (gemm_step, lazy_step or None).
+    """
+    if out != "" or len(path) < 2:
+        return None
+    entries: list[tuple[str, tuple]] = [(t, ("in", k)) for k, t in enumerate(terms)]
+    step_ops = []
+    for s, (i, j) in enumerate(path):
+        step_ops.append((entries[i], entries[j]))
+        entries = [e for k, e in enumerate(entries) if k != i and k != j] + [(names[s], ("st", s))]
+    (ta, oa), (tb, ob) = step_ops[-1]
+    if set(ta) != set(tb) or len(set(ta)) != len(ta) or len(set(tb)) != len(tb):
+        return None
+
+    def gemm_shaped(s):
+        (t1, _), (t2, _) = step_ops[s]
+        return bool((set(t1) & set(t2)) - set(names[s]))
+
+    def outer(s):
+        (t1, _), (t2, _) = step_ops[s]
+        return not (set(t1) & set(t2)) and set(names[s]) == set(t1) | set(t2)
+
+    cands = [(o, other) for o, other in ((oa, ob), (ob, oa)) if o[0] == "st" and gemm_shaped(o[1])]
+    if not cands:
+        return None
+    g_origin, other = max(cands, key=lambda c: c[0][1])
+    lazy = other[1] if other[0] == "st" and outer(other[1]) else None
+    return g_origin[1], lazy
+
+
 def _execute_path(
     terms: list[str],
     out: str,
@@ -198,24 +235,58 @@ def _execute_path(
 
     Each step contracts ``ops[i]`` and ``ops[j]`` on the HIP engine, removes
     both and appends the result; the last step produces ``out`` and carries
-    the alpha/beta epilogue.
+    the alpha/beta epilogue. A final full dot is fused into the GEMM that
+    produces one of its operands (see ``_fusion_plan``): the 21 GB product and
+    outer product of 'ia,jb,abP,ijP->' are never written.
     """
     names = _path_names(terms, out, path)
+    plan = _fusion_plan(terms, out, path, names)
+    deferred = set() if plan is None else {s for s in plan if s is not None}
     cur_terms = list(terms)
-    cur = list(ops)
+    cur: list = list(ops)
     for s, (i, j) in enumerate(path):
         last = s == len(path) - 1
-        res = engine.contract(
-            [cur_terms[i], cur_terms[j]],
-            names[s],
-            [cur[i], cur[j]],
-            alpha if last else 1.0,
-            beta if last else 0.0,
-            C if last else None,
-        )
+        ti, tj = cur_terms[i], cur_terms[j]
+        if s in deferred:
+            res = ("deferred", s, [ti, tj], [cur[i], cur[j]])
+        elif last and plan is not None:
+            res = _fused_dot(names, plan, ti, cur[i], tj, cur[j], alpha, beta, C)
+        else:
+            res = engine.contract(
+                [ti, tj],
+                names[s],
+                [_materialise(names, cur[i]), _materialise(names, cur[j])],
+                alpha if last else 1.0,
+                beta if last else 0.0,
+                C if last else None,
+            )
         cur = [t for k, t in enumerate(cur) if k != i and k != j] + [res]
         cur_terms = [t for k, t in enumerate(cur_terms) if k != i and k != j] + [names[s]]
     return cur[0]
+
+
+def _materialise(names, x):
+    """A deferred step's result as a tensor (computed now)."""
+    if isinstance(x, tuple):
+        _, s, tt, tensors = x
+        return engine.contract(tt, names[s], [_materialise(names, t) for t in tensors])
+    return x
+
+
+def _fused_dot(names, plan, ti, xi, tj, xj, alpha, beta, C):
+    """Final full dot with one operand produced by the deferred GEMM step."""
+    gs, lazy = plan
+    g, other, t_other = (xi, xj, tj) if isinstance(xi, tuple) and xi[1] == gs else (xj, xi, ti)
+    _, _, gterms, gtensors = g
+    gtensors = [_materialise(names, t) for t in gtensors]
+    if isinstance(other, tuple) and other[1] == lazy:
+        factors = list(zip(other[2], [_materialise(names, t) for t in other[3]]))
+    else:
+        factors = [(t_other, _materialise(names, other))]
+    res = engine.contract_gemm_dot(gterms, names[gs], gtensors, factors, alpha, beta, C)
+    if res is not None:
+        return res
+    return engine.contract([ti, tj], "", [_materialise(names, xi), _materialise(names, xj)], alpha, beta, C)
 
 
 def multi_einsum(*contractions: tuple) -> list[torch.Tensor]:

@@ -35,6 +35,12 @@ SIGNATURES = {
         _int,
         [_int, _int, _int, _i64, _i64, _i64, _dbl, _vp, _i64, _i64, _vp, _i64, _i64, _dbl, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp],
     ),
+    "tt_gemm_dot_workspace_bytes": (_sz, [_int, _i64, _i64, _i64]),
+    "tt_gemm_dot": (
+        _int,
+        [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64p, _vp, _i64p,
+         _dbl, _dbl, _vp, _vp, _vp, _sz, _vp],
+    ),
     "tt_mp2_energy_workspace_bytes": (_sz, [_int, _i64, _i64, _i64]),
     "tt_mp2_energy": (_int, [_int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _int, _vp]),
     "tt_ao_to_mo_workspace_bytes": (_sz, [_int, _i64, _i64, _i64, _i64]),

@@ -503,3 +503,90 @@ def contract(
         C,
     )
     return D
+
+
+# ---------------------------------------------------------------------------
+# GEMM with a dot epilogue (a product contracted with E on the spot)
+# ---------------------------------------------------------------------------
+def contract_gemm_dot(
+    terms: list[str],
+    xname: str,
+    tensors: list[torch.Tensor],
+    factors: list[tuple[str, torch.Tensor]],
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+) -> torch.Tensor | None:
+    """sum over X * E with X = einsum(terms -> xname)(tensors) never stored, via tt_gemm_dot.
+
+    E is the product of the factor tensors, whose letters together are X's
+    letters (one factor: a tensor in X's letters; two: an outer product that
+    is never materialised either). Returns a 0-D tensor, or None when the
+    contraction has no GEMM shape or its letter groups exceed what the fused
+    kernel decodes (batch <= 1 letter, M and N <= 2 letters each).
+    """
+    ops = [Operand(t, x) for t, x in zip(terms, tensors)]
+    A, B = ops
+    la, lb, lo = set(A.letters), set(B.letters), set(xname)
+    kl = [c for c in A.letters if c in lb and c not in lo]
+    batch = [c for c in xname if c in la and c in lb]
+    ml = [c for c in xname if c in la and c not in lb]
+    nl = [c for c in xname if c in lb and c not in la]
+    facs = [Operand(t, x) for t, x in factors]
+    if not kl or len(batch) > 1 or len(ml) > 2 or len(nl) > 2 or not 1 <= len(facs) <= 2:
+        return None
+    if set().union(*[set(f.letters) for f in facs]) != lo or len(xname) != len(lo):
+        return None
+    dt, dev = A.t.dtype, A.t.device
+    code = dtype_code(dt)
+    for idx, (op, other) in enumerate(((A, lb), (B, la))):
+        gone = [c for c in op.letters if c not in other and c not in lo]
+        if gone:
+            keep = [c for c in op.letters if c not in gone]
+            R = torch.empty([op.ext[c] for c in keep], dtype=dt, device=dev)
+            strided_contract([(op.ext[c], op.strd[c], 0) for c in keep], [(op.ext[c], op.strd[c], 0) for c in gone], op.t, None, R)
+            ops[idx] = Operand("".join(keep), R)
+    A, B = ops
+    kl.sort(key=lambda c: -A.strd[c])
+    ext = {**A.ext, **B.ext}
+    nb = _numel(ext[c] for c in batch)
+    M = _numel(ext[c] for c in ml)
+    N = _numel(ext[c] for c in nl)
+    K = _numel(ext[c] for c in kl)
+    la_ = _gemm_layout(A, ml, kl)
+    gba = _merge(A, batch)
+    if la_ is None or gba is None:
+        A = Operand("".join(batch + ml + kl), pack(A, batch + ml + kl))
+        la_, gba = (True, max(K, 1)), (nb, M * K)
+    lb_ = _gemm_layout(B, nl, kl)
+    gbb = _merge(B, batch)
+    if lb_ is None or gbb is None:
+        B = Operand("".join(batch + kl + nl), pack(B, batch + kl + nl))
+        lb_, gbb = (False, max(N, 1)), (nb, K * N)
+    sA = gba[1] if nb > 1 else 0
+    sB = gbb[1] if nb > 1 else 0
+
+    m_hi = ml[0] if len(ml) == 2 else None
+    m_lo = ml[-1] if ml else None
+    n_hi = nl[0] if len(nl) == 2 else None
+    n_lo = nl[-1] if nl else None
+    b_l = batch[0] if batch else None
+
+    def strides(f: Operand):
+        return _lib.i64_array([0 if c is None else f.strd.get(c, 0) for c in (m_hi, m_lo, n_hi, n_lo, b_l)])
+
+    lib = _lib.load()
+    e1 = facs[0]
+    e2 = facs[1] if len(facs) == 2 else None
+    wsb = lib.tt_gemm_dot_workspace_bytes(code, M, N, nb)
+    ws = _workspace(wsb, dev)
+    out = torch.empty((), dtype=dt, device=dev)
+    st = lib.tt_gemm_dot(
+        code, int(not la_[0]), int(lb_[0]), M, N, K,
+        _ptr(A.t), la_[1], sA, _ptr(B.t), lb_[1], sB, nb,
+        ext[m_lo] if m_lo else 1, ext[n_lo] if n_lo else 1,
+        _ptr(e1.t), strides(e1), None if e2 is None else _ptr(e2.t), None if e2 is None else strides(e2),
+        float(alpha), float(beta), _ptr(C), _ptr(out), _ptr(ws), wsb, _stream_ptr(dev),
+    )
+    _lib.check(st, "tt_gemm_dot")
+    return out
