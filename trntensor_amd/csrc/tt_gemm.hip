@@ -28,16 +28,20 @@ constexpr int kThreads = 256;
 
 // One operand's ROWS x 16 stage: global -> registers -> LDS, plus fragment reads.
 // KC: element (row, k) at p[row * ld + k]; otherwise at p[k * ld + row].
-// Each thread stages E = ROWS / 16 elements that are contiguous in memory and
-// in LDS (one address per operand, NC 16-byte pieces at immediate offsets):
-//   KC: row t / (16 / E), k from (t % (16 / E)) E;   RC: k t / 16, rows from (t % 16) E.
+// Each thread stages E = ROWS / 16 elements as NC 16-byte pieces from one
+// address at immediate offsets:
+//   KC: row t / (16 / E), one contiguous chunk from k = (t % (16 / E)) E;
+//   RC: k-row t / 16, pieces (t % 16) + 16 c, so every instruction covers 256
+//       contiguous bytes of the k-row (coalesced loads, conflict-free stores).
+// RC k-rows are padded by 4 elements: the four lane groups of a fragment read
+// (k-rows 4 g + s) then land on disjoint LDS banks.
 template <typename T, int ROWS, bool KC, bool VEC>
 struct Stage {
     static constexpr int V = Vec16<T>::n;
     static constexpr int E = ROWS * kBK / kThreads;
     static constexpr int NC = E / V;  // 16-byte pieces per thread
     static constexpr int PAD = 16 / sizeof(T);
-    static constexpr int PITCH = KC ? (kBK + PAD) : (ROWS + PAD);
+    static constexpr int PITCH = KC ? (kBK + PAD) : (ROWS + 4);
     static constexpr int ELEMS = KC ? ROWS * PITCH : kBK * PITCH;
     static_assert(E % V == 0 && E <= kBK * (KC ? 1 : ROWS), "stage split");
     typedef typename Vec16<T>::type vec_t;
@@ -50,10 +54,14 @@ struct Stage {
             row = t / (kBK / E);
             k = (t % (kBK / E)) * E;
         } else {
-            k = t / (ROWS / E);
-            row = (t % (ROWS / E)) * E;
+            // 16 threads per k-row; a thread's NC pieces sit 16 pieces apart so
+            // each instruction covers 256 contiguous bytes of the row.
+            k = t / 16;
+            row = (t % 16) * V;
         }
     }
+    // Element offset (along the contiguous direction) of piece c relative to piece 0.
+    __device__ __forceinline__ static constexpr int piece(int c) { return KC ? c * V : c * 16 * V; }
 
     // FAST (interior stage: tile inside the matrix, 16-byte aligned):
     // unconditional vector loads. Otherwise element-wise loads from clamped
@@ -67,13 +75,13 @@ struct Stage {
         if (FAST) {
             const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) reg[c] = reinterpret_cast<const vec_t*>(src)[c];
+            for (int c = 0; c < NC; ++c) reg[c] = *reinterpret_cast<const vec_t*>(src + piece(c));
         } else {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
-                    const int off = c * V + e;
+                    const int off = piece(c) + e;
                     const int64_t gr = row0 + r + (KC ? 0 : off);
                     const int64_t gk = k0 + k + (KC ? off : 0);
                     const bool ok = gr < rows && gk < kdim;
@@ -87,9 +95,9 @@ struct Stage {
     __device__ __forceinline__ void store(T* s) const {
         int r, k;
         place(r, k);
-        vec_t* dst = reinterpret_cast<vec_t*>(KC ? (s + r * PITCH + k) : (s + k * PITCH + r));
+        T* dst = KC ? (s + r * PITCH + k) : (s + k * PITCH + r);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) dst[c] = reg[c];
+        for (int c = 0; c < NC; ++c) *reinterpret_cast<vec_t*>(dst + piece(c)) = reg[c];
     }
 
     // The four k values (MFMA steps 0..3) this lane feeds for the 16-row block at rb.
