@@ -304,3 +304,50 @@ class TestPathFusion:
         path = [(0, 1), (0, 1), (0, 1)]
         names = _path_names(["ia", "jb", "abP", "ijP"], "", path)
         assert _fusion_plan(["ia", "jb", "abP", "ijP"], "", path, names) == (1, 0)
+
+
+class TestOptimalPath:
+    """einsum(optimize="optimal"): the opt-in fewest-multiply-add order gives the
+    reference path executor's value (oracle, greedy order) within a bar scaled
+    by the same contraction over absolute values."""
+
+    @staticmethod
+    def check(sub, shapes, dt=torch.float64, seed=0):
+        g = torch.Generator().manual_seed(seed)
+        ops = [torch.randn(*s, generator=g, dtype=torch.float64).to(dt) for s in shapes]
+        got = trntensor.einsum(sub, *[o.cuda() for o in ops], optimize="optimal")
+        ref = cpu_ref.einsum(sub, *[o.double() for o in ops])
+        scale = torch.einsum(sub, *[o.double().abs() for o in ops])
+        bar = 1e-13 if dt == torch.float64 else 1e-5
+        assert got.dtype == dt and tuple(got.shape) == tuple(ref.shape)
+        err = (got.cpu().double() - ref).abs()
+        assert bool((err <= bar * (scale + 1e-300)).all()), float((err / (scale + 1e-300)).max())
+
+    def test_config5_small(self, hip):
+        self.check("ia,jb,abP,ijP->", [(12, 20), (10, 20), (20, 20, 30), (12, 10, 30)])
+
+    def test_chain(self, hip):
+        self.check("ij,jk,kl,lm->im", [(30, 200), (200, 5), (5, 150), (150, 40)], seed=1)
+
+    def test_chain_fp32(self, hip):
+        self.check("ij,jk,kl,lm->im", [(30, 200), (200, 5), (5, 150), (150, 40)], dt=torch.float32, seed=2)
+
+    def test_mp2_like(self, hip):
+        self.check("iaP,jbP,ia,jb->ij", [(6, 24, 40), (6, 24, 40), (6, 24), (6, 24)], seed=3)
+
+    def test_config5_full(self, hip):
+        """BASELINE config 5 at full size: optimal order needs 2.16e10 multiply-adds
+        instead of 2.1e12; checked against the fp64 greedy-order result on the GPU
+        (the oracle takes minutes at this size)."""
+        g = torch.Generator().manual_seed(0)
+        A = (torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1).cuda()
+        B = (torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1).cuda()
+        W = (torch.randn(400, 400, 800, generator=g, dtype=torch.float64) * 0.01).cuda()
+        V = (torch.randn(128, 128, 800, generator=g, dtype=torch.float64) * 0.1).cuda()
+        plan = trntensor.plan_contraction("ia,jb,abP,ijP->", A, B, W, V, optimize="optimal")
+        assert plan.contraction_path == [(1, 2), (1, 2), (0, 1)]
+        fast = trntensor.einsum("ia,jb,abP,ijP->", A, B, W, V, optimize="optimal")
+        slow = trntensor.einsum("ia,jb,abP,ijP->", A, B, W, V)
+        # |sum| bound: the same contraction over absolute values, via the cheap order
+        scale = trntensor.einsum("ia,jb,abP,ijP->", A.abs(), B.abs(), W.abs(), V.abs(), optimize="optimal")
+        assert abs(float(fast) - float(slow)) <= 1e-13 * float(scale)

@@ -196,3 +196,100 @@ def test_path_layout_choice_config5():
     assert _step_output(["ia", "jb", "abP", "ijP"], 0, 1, "") == "iajb"
     # chains keep the reference's names
     assert _path_names(["ij", "jk", "kl"], "il", [(1, 2), (0, 1)]) == ["jl", "il"]
+
+
+class TestOptimalPath:
+    """optimize="optimal" (opt-in; no counterpart in the reference): the DP path
+    is pinned against brute force over every pairwise order, checked to be a
+    valid path by executing it on the CPU, and never costs more than greedy."""
+
+    @staticmethod
+    def _all_paths(n):
+        if n <= 2:
+            yield [(0, 1)]
+            return
+        for i in range(n - 1):
+            for j in range(i + 1, n):
+                for rest in TestOptimalPath._all_paths(n - 1):
+                    yield [(i, j)] + rest
+
+    @staticmethod
+    def _sizes(terms, ops):
+        return {c: int(n) for term, op in zip(terms, ops) for c, n in zip(term, op.shape)}
+
+    def test_config5_closed_form(self):
+        from trntensor_amd.plan import _optimal_path_search, path_cost
+
+        terms, sizes = ["ia", "jb", "abP", "ijP"], dict(i=128, j=128, a=400, b=400, P=800)
+        path = _optimal_path_search(terms, "", sizes)
+        # jb.abP -> ajP (i a b P... = 128*400*400*800), ijP.ajP -> ia (128*128*800*400), ia.ia -> ''
+        assert path == [(1, 2), (1, 2), (0, 1)]
+        assert path_cost(terms, "", sizes, path) == 128 * 400 * 400 * 800 + 128 * 128 * 800 * 400 + 128 * 400
+        greedy = _greedy_path_search(terms, "", sizes)
+        # ia.jb -> abij, abP.ijP -> abij, abij.abij -> ''
+        assert path_cost(terms, "", sizes, greedy) == 2 * 128 * 400 * 128 * 400 + 128 * 128 * 400 * 400 * 800
+
+    def test_matches_brute_force(self):
+        from trntensor_amd.plan import _optimal_path_search, path_cost
+
+        rng = random.Random(7)
+        checked = 0
+        while checked < 150:
+            sub, ops = _random_expression(rng)
+            lhs, out = _parse_subscripts(sub)
+            terms = lhs.split(",")
+            if not 3 <= len(terms) <= 5:
+                continue
+            sizes = self._sizes(terms, ops)
+            path = _optimal_path_search(terms, out, sizes)
+            assert len(path) == len(terms) - 1 and path[-1] == (0, 1), sub
+            best = min(path_cost(terms, out, sizes, p) for p in self._all_paths(len(terms)))
+            assert path_cost(terms, out, sizes, path) == best, sub
+            assert best <= path_cost(terms, out, sizes, _greedy_path_search(terms, out, sizes)), sub
+            checked += 1
+
+    def test_path_executes_to_einsum(self):
+        """The optimal path, run by the oracle's pairwise executor, gives einsum's value."""
+        rng = random.Random(11)
+        gen = torch.Generator().manual_seed(3)
+        checked = 0
+        while checked < 60:
+            sub, ops = _random_expression(rng)
+            if len(ops) < 3:
+                continue
+            ops = [torch.randn(*o.shape, generator=gen, dtype=torch.float64) for o in ops]
+            trntensor.clear_plan_cache()
+            plan = trntensor.plan_contraction(sub, *ops, optimize="optimal")
+            ref_plan = cpu_ref.plan_contraction(sub, *ops)
+            ref_plan.contraction_path = plan.contraction_path
+            got = cpu_ref.execute_path(sub, ops, ref_plan)
+            want = torch.einsum(sub, *ops)
+            assert torch.allclose(got, want, rtol=1e-10, atol=1e-10), sub
+            checked += 1
+
+    def test_large_operand_count_falls_back(self):
+        from trntensor_amd.plan import OPTIMAL_MAX_OPERANDS, _optimal_path_search, path_cost
+
+        rng = random.Random(5)
+        n = OPTIMAL_MAX_OPERANDS + 2
+        letters = "abcdefghijklmn"
+        terms = [letters[k] + letters[k + 1] for k in range(n)]  # a matrix chain
+        sizes = {c: rng.randint(2, 60) for c in letters}
+        out = letters[0] + letters[n]
+        path = _optimal_path_search(terms, out, sizes)
+        assert len(path) == n - 1 and path[-1] == (0, 1)
+        assert path_cost(terms, out, sizes, path) <= path_cost(terms, out, sizes, _greedy_path_search(terms, out, sizes))
+
+    def test_default_and_cache(self):
+        ops = (t(128, 400), t(128, 400), t(400, 400, 800), t(128, 128, 800))
+        trntensor.clear_plan_cache()
+        g = trntensor.plan_contraction("ia,jb,abP,ijP->", *ops)
+        o = trntensor.plan_contraction("ia,jb,abP,ijP->", *ops, optimize="optimal")
+        assert g.contraction_path == [(0, 1), (0, 1), (0, 1)]
+        assert o.contraction_path == [(1, 2), (1, 2), (0, 1)]
+        assert trntensor.plan_cache_info()["size"] == 2
+        assert trntensor.plan_contraction("ia,jb,abP,ijP->", *ops, optimize="optimal") is o
+        # two operands: the label does not depend on the search
+        assert trntensor.plan_contraction("ij,jk->ik", t(4, 3), t(3, 5), optimize="optimal").strategy == "matmul"
+        with pytest.raises(ValueError, match="optimize must be"):
+            trntensor.plan_contraction("ij,jk->ik", t(4, 3), t(3, 5), optimize="dp")

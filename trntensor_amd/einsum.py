@@ -46,6 +46,7 @@ def einsum(
     out: torch.Tensor | None = None,
     dtype: str | torch.dtype | None = None,
     precision: str = "fast",
+    optimize: str = "greedy",
 ) -> torch.Tensor:
     """Einstein summation with contraction planning, executed on MI355X.
 
@@ -55,6 +56,8 @@ def einsum(
     ``precision="kahan"`` contracts in float64 and returns the first operand's
     dtype; ``"dd"`` raises ``NotImplementedError``. The result lives on the
     first operand's device: CPU operands are staged through the GPU.
+    ``optimize`` selects the path search for 3+ operands: ``"greedy"`` (the
+    reference's order, default) or ``"optimal"`` (fewest multiply-adds; opt-in).
 
     Examples::
 
@@ -67,7 +70,7 @@ def einsum(
     target = _resolve_dtype(dtype)
     if target is not None:
         operands = tuple(op.to(target) for op in operands)
-    plan = plan_contraction(subscripts, *operands, precision=precision)
+    plan = plan_contraction(subscripts, *operands, precision=precision, optimize=optimize)
     return _execute_contraction(subscripts, operands, plan, alpha=alpha, beta=beta, out=out)
 
 
@@ -145,43 +148,48 @@ def _path_names(terms: list[str], out: str, path: list[tuple[int, int]]) -> list
     """Letter order of every intermediate.
 
     Starts from the reference's naming. An intermediate's letter order is not
-    observable (only the final output's is), so when a step contracts two
-    tensors with the same letter set (a full or elementwise dot), the
-    operand produced earlier takes the other operand's order: the step then
-    streams both tensors contiguously instead of one of them transposed.
+    observable (only the final output's is), so it is chosen for the step
+    that consumes it: the letters summed in that step must form one run in
+    the partner operand's order, or the GEMM would first pack the
+    intermediate. When they do not, the intermediate keeps its other letters
+    in order and takes the summed letters last, in the partner's order. This
+    covers a full or elementwise dot (every letter summed: the intermediate
+    takes the partner's order and the step streams both tensors
+    contiguously). When both operands of a step are intermediates, the one
+    produced earlier is reordered. Each intermediate is consumed exactly
+    once, so steps are visited from the last to the first.
     """
     names: list[str] = []
     cur = list(terms)
+    entries: list[tuple[str, int]] = [("in", k) for k in range(len(terms))]
+    step_ops = []
     for s, (i, j) in enumerate(path):
+        step_ops.append((entries[i], entries[j]))
         name = out if s == len(path) - 1 else _step_output(cur, i, j, out)
         names.append(name)
         cur = [t for k, t in enumerate(cur) if k != i and k != j] + [name]
+        entries = [e for k, e in enumerate(entries) if k != i and k != j] + [("st", s)]
 
-    for _ in range(len(path)):
-        changed = False
-        cur = list(terms)
-        src: list[int | None] = [None] * len(terms)  # producing step of each entry
-        for s, (i, j) in enumerate(path):
-            ti, tj = cur[i], cur[j]
-            if (
-                len(set(ti)) == len(ti)
-                and len(set(tj)) == len(tj)
-                and set(ti) == set(tj)
-                and ti != tj
-            ):
-                pi, pj = src[i], src[j]
-                # rename the earlier-produced intermediate (never the final output)
-                cands = [(p, other) for p, other in ((pi, tj), (pj, ti)) if p is not None]
-                if cands:
-                    p, other = min(cands, key=lambda x: x[0])
-                    names[p] = other
-                    changed = True
-                    break
-            name = names[s]
-            cur = [t for k, t in enumerate(cur) if k != i and k != j] + [name]
-            src = [x for k, x in enumerate(src) if k != i and k != j] + [s]
-        if not changed:
-            break
+    def name_of(e):
+        return terms[e[1]] if e[0] == "in" else names[e[1]]
+
+    for t in reversed(range(len(path))):
+        ei, ej = step_ops[t]
+        inter = [e for e in (ei, ej) if e[0] == "st"]
+        if not inter:
+            continue
+        x = min(inter, key=lambda e: e[1])
+        partner = ej if x is ei else ei
+        xn, pn = name_of(x), name_of(partner)
+        if len(set(pn)) != len(pn):
+            continue
+        summed = (set(xn) & set(pn)) - set(names[t])
+        if not summed:
+            continue
+        order = "".join(c for c in pn if c in summed)
+        if order in (xn[: len(order)], xn[len(xn) - len(order):]):
+            continue  # already one run, in the partner's order, at an end
+        names[x[1]] = "".join(c for c in xn if c not in summed) + order
     return names
 
 

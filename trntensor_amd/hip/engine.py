@@ -304,23 +304,64 @@ def gemm(
     _lib.check(st, "tt_gemm")
 
 
+def split_k(M: int, N: int, K: int, batch: int) -> int:
+    """K-slices for a GEMM whose output tiles cannot fill the chip.
+
+    A launch with fewer than ~200 128x128 output tiles leaves most of the
+    256 CUs idle however long K is; slicing K (each slice >= 512 deep) into
+    batch entries gives ~512 workgroups. Only unbatched GEMMs with K >= 4096
+    are split.
+    """
+    if batch > 1 or K < 4096:
+        return 1
+    tiles = (-(-M // 128)) * (-(-N // 128))
+    if tiles >= 192:
+        return 1
+    return max(1, min(-(-512 // tiles), K // 512))
+
+
+def _k_step(k_contiguous: bool, ld: int) -> int:
+    """Element distance between consecutive k of an operand viewed rows x K."""
+    return 1 if k_contiguous else ld
+
+
 class _GemmRecipe:
-    """Launch parameters of a contraction that maps onto one tt_gemm call with
-    both operands in place; `swap` means the output is computed as B^T A^T."""
+    """Launch parameters of a contraction that maps onto tt_gemm with both
+    operands in place; `swap` means the output is computed as B^T A^T.
 
-    __slots__ = ("swap", "ta", "tb", "M", "N", "K", "lda", "sA", "ldb", "sB", "ldd", "sD", "batch", "shape", "dt")
+    split > 1 slices K into `split` batch entries of a [split, M, N]
+    temporary (slice s reads k in [s*kc, (s+1)*kc), a last shorter slice goes
+    in a second launch), summed in slice order into D by one strided pass
+    that also applies alpha/beta. D is then [M][N] contiguous."""
 
-    def __init__(self, swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, batch, shape, dt):
+    __slots__ = ("swap", "ta", "tb", "M", "N", "K", "lda", "sA", "ldb", "sB", "ldd", "sD", "batch", "shape", "dt",
+                 "split")
+
+    def __init__(self, swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, batch, shape, dt, split=1):
         self.swap, self.ta, self.tb = swap, ta, tb
         self.M, self.N, self.K = M, N, K
         self.lda, self.sA, self.ldb, self.sB, self.ldd, self.sD = lda, sA, ldb, sB, ldd, sD
         self.batch, self.shape, self.dt = batch, shape, dt
+        self.split = split
 
     def run(self, At, Bt, alpha, beta, C):
         D = torch.empty(self.shape, dtype=self.dt, device=At.device)
         X, Y = (Bt, At) if self.swap else (At, Bt)
-        gemm(self.ta, self.tb, self.M, self.N, self.K, X, self.lda, self.sA, Y, self.ldb, self.sB, D,
-             self.ldd, self.sD, self.batch, alpha, beta, C, self.ldd, self.sD)
+        if self.split <= 1:
+            gemm(self.ta, self.tb, self.M, self.N, self.K, X, self.lda, self.sA, Y, self.ldb, self.sB, D,
+                 self.ldd, self.sD, self.batch, alpha, beta, C, self.ldd, self.sD)
+            return D
+        M, N, K = self.M, self.N, self.K
+        kc = -(-K // self.split)
+        full, rem = K // kc, K % kc
+        ka = _k_step(not self.ta, self.lda)  # X[m*lda + k] unless transposed
+        kb = _k_step(self.tb, self.ldb)  # Y[n*ldb + k] when transposed
+        T = torch.empty((full + (rem > 0), M, N), dtype=self.dt, device=At.device)
+        gemm(self.ta, self.tb, M, N, kc, X, self.lda, kc * ka, Y, self.ldb, kc * kb, T, N, M * N, full)
+        if rem:
+            gemm(self.ta, self.tb, M, N, rem, X, self.lda, 0, Y, self.ldb, 0, T[full], N, 0, 1,
+                 a_off=full * kc * ka, b_off=full * kc * kb)
+        strided_contract([(M, N, 0), (N, 1, 0)], [(T.shape[0], M * N, 0)], T, None, D, alpha, beta, C)
         return D
 
 
@@ -349,6 +390,85 @@ def _gemm_layout(op: Operand, rows: list[str], ks: list[str]):
     return None
 
 
+def _merge_strides(ext: dict, strd: dict, letters: list[str]) -> tuple[int, int] | None:
+    """_merge on plain extent/stride maps (letters absent from `strd` have stride 0)."""
+    extent, stride = 1, 0
+    for c in reversed(letters):
+        n, s = ext[c], strd.get(c, 0)
+        if n == 1:
+            continue
+        if extent == 1:
+            extent, stride = n, s
+        elif s == stride * extent:
+            extent *= n
+        else:
+            return None
+    return extent, stride
+
+
+def _inplace_mappings(A: Operand, B: Operand, out: str, batch, ml, nl, kl, ext):
+    """Yield GEMM mappings that use both operands and the output in place.
+
+    The output is contiguous in `out` order. Each candidate assigns letters to
+    (batch, M, N); a mapping is kept when A's M and K groups, B's N and K
+    groups and every group of the output each collapse to one stride, and
+    the output has N (direct) or M (swapped) unit-stride. Besides the plain
+    grouping, an unbatched contraction may move one M letter (or N letter)
+    into the batch, read with stride 0 by the other operand: a broadcast
+    batch, which replaces packing an operand whose M or N letters are split
+    by a K letter (e.g. 'jb,abP->jaP' runs as a batch over a).
+    Yields (swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, nb).
+    """
+    dstrd: dict[str, int] = {}
+    acc = 1
+    for c in reversed(out):
+        dstrd[c] = acc
+        acc *= ext[c]
+    cands = [(batch, ml, nl)]
+    if not batch:
+        # a peel must not leave a sliver M or N (MFMA tiles are 64+ wide)
+        M0, N0 = _numel(ext[c] for c in ml), _numel(ext[c] for c in nl)
+        cands += [([x], [c for c in ml if c != x], nl) for x in ml
+                  if ext[x] > 1 and M0 // ext[x] >= min(16, M0)]
+        cands += [([x], ml, [c for c in nl if c != x]) for x in nl
+                  if ext[x] > 1 and N0 // ext[x] >= min(16, N0)]
+    K = _numel(ext[c] for c in kl)
+    for bl, m_, n_ in cands:
+        la = _gemm_layout(A, m_, kl)
+        lb = _gemm_layout(B, n_, kl)
+        if la is None or lb is None:
+            continue
+        nb = _numel(ext[c] for c in bl)
+        ga = _merge_strides(ext, A.strd, bl)
+        gb = _merge_strides(ext, B.strd, bl)
+        gd = _merge_strides(ext, dstrd, bl)
+        dm = _merge_strides(ext, dstrd, m_)
+        dn = _merge_strides(ext, dstrd, n_)
+        if None in (ga, gb, gd, dm, dn):
+            continue
+        sA, sB, sD = (ga[1], gb[1], gd[1]) if nb > 1 else (0, 0, 0)
+        M = _numel(ext[c] for c in m_)
+        N = _numel(ext[c] for c in n_)
+        if N == 1 or dn[1] == 1:
+            ldd = dm[1] if M > 1 else max(N, 1)
+            if M <= 1 or ldd >= N:
+                yield (0, not la[0], lb[0], M, N, K, la[1], sA, lb[1], sB, ldd, sD, nb)
+        if M == 1 or dm[1] == 1:
+            ldd = dn[1] if N > 1 else max(M, 1)
+            if N <= 1 or ldd >= M:
+                yield (1, not lb[0], la[0], N, M, K, lb[1], sB, la[1], sA, ldd, sD, nb)
+
+
+def _inplace_recipe(A, B, out, batch, ml, nl, kl, ext, dt) -> _GemmRecipe | None:
+    """The first in-place mapping (see _inplace_mappings) as a recipe, with
+    K split when the output alone cannot fill the chip."""
+    shape = [ext[c] for c in out]
+    for swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, nb in _inplace_mappings(A, B, out, batch, ml, nl, kl, ext):
+        split = split_k(M, N, K, nb) if ldd == max(N, 1) else 1
+        return _GemmRecipe(swap, ta, tb, M, N, K, lda, sA, ldb, sB, ldd, sD, nb, shape, dt, split)
+    return None
+
+
 def contract_gemm(
     A: Operand,
     B: Operand,
@@ -369,6 +489,12 @@ def contract_gemm(
     """
     dev, dt = A.t.device, A.t.dtype
     ext = {**A.ext, **B.ext}
+    rec = _inplace_recipe(A, B, out, batch, ml, nl, kl, ext, dt)
+    if rec is not None:
+        if recipe_key is not None:
+            _RECIPES[recipe_key] = rec
+        return rec.run(A.t, B.t, alpha, beta, C)
+
     nb = _numel(ext[c] for c in batch)
     M = _numel(ext[c] for c in ml)
     N = _numel(ext[c] for c in nl)
@@ -570,7 +696,7 @@ def contract_gemm_dot(
     m_lo = ml[-1] if ml else None
     n_hi = nl[0] if len(nl) == 2 else None
     n_lo = nl[-1] if nl else None
-    b_l = batch[0] if batch else None
+    b_l = batch[0] if batch and nb > 1 else None  # K-slices reuse the batch index with E stride 0
 
     def strides(f: Operand):
         return _lib.i64_array([0 if c is None else f.strd.get(c, 0) for c in (m_hi, m_lo, n_hi, n_lo, b_l)])
@@ -578,15 +704,34 @@ def contract_gemm_dot(
     lib = _lib.load()
     e1 = facs[0]
     e2 = facs[1] if len(facs) == 2 else None
-    wsb = lib.tt_gemm_dot_workspace_bytes(code, M, N, nb)
-    ws = _workspace(wsb, dev)
     out = torch.empty((), dtype=dt, device=dev)
-    st = lib.tt_gemm_dot(
-        code, int(not la_[0]), int(lb_[0]), M, N, K,
-        _ptr(A.t), la_[1], sA, _ptr(B.t), lb_[1], sB, nb,
-        ext[m_lo] if m_lo else 1, ext[n_lo] if n_lo else 1,
-        _ptr(e1.t), strides(e1), None if e2 is None else _ptr(e2.t), None if e2 is None else strides(e2),
-        float(alpha), float(beta), _ptr(C), _ptr(out), _ptr(ws), wsb, _stream_ptr(dev),
-    )
-    _lib.check(st, "tt_gemm_dot")
+    es = A.t.element_size()
+
+    def launch(kk, nbat, sa, sb, a_off, b_off, beta_, C_):
+        wsb = lib.tt_gemm_dot_workspace_bytes(code, M, N, nbat)
+        ws = _workspace(wsb, dev)
+        st = lib.tt_gemm_dot(
+            code, int(not la_[0]), int(lb_[0]), M, N, kk,
+            ctypes.c_void_p(A.t.data_ptr() + a_off * es), la_[1], sa,
+            ctypes.c_void_p(B.t.data_ptr() + b_off * es), lb_[1], sb, nbat,
+            ext[m_lo] if m_lo else 1, ext[n_lo] if n_lo else 1,
+            _ptr(e1.t), strides(e1), None if e2 is None else _ptr(e2.t), None if e2 is None else strides(e2),
+            float(alpha), float(beta_), _ptr(C_), _ptr(out), _ptr(ws), wsb, _stream_ptr(dev),
+        )
+        _lib.check(st, "tt_gemm_dot")
+
+    split = split_k(M, N, K, nb)
+    if split <= 1:
+        launch(K, nb, sA, sB, 0, 0, beta, C)
+        return out
+    # The dot is linear in the product, so K-slices (batch entries whose E
+    # batch stride is 0) each contribute partials to the same sum; a last
+    # shorter slice adds its share onto the first launch's result.
+    kc = -(-K // split)
+    full, rem = K // kc, K % kc
+    ka = _k_step(la_[0], la_[1])
+    kb = _k_step(lb_[0], lb_[1])
+    launch(kc, full, kc * ka, kc * kb, 0, 0, beta, C)
+    if rem:
+        launch(rem, 1, 0, 0, full * kc * ka, full * kc * kb, 1.0, out)
     return out

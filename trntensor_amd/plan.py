@@ -96,13 +96,20 @@ def _validate_subscripts(subscripts: str, operands: tuple) -> None:
 
 _PLAN_CACHE: dict[tuple, ContractionPlan] = {}
 
+# Path searches for 3+ operands. "greedy" is the reference's rule and the
+# default; "optimal" is opt-in (no counterpart in the reference).
+PATH_SEARCHES = ("greedy", "optimal")
 
-def _shape_key(subscripts: str, operands: tuple, precision: str = "fast") -> tuple:
+
+def _shape_key(subscripts: str, operands: tuple, precision: str = "fast", optimize: str = "greedy") -> tuple:
     """Cache key: subscripts, operand shapes, precision (reference plan.py:119-123).
 
-    dtype and device are not part of the key, as in the reference.
+    dtype and device are not part of the key, as in the reference. A
+    non-default path search is appended, so default keys keep the
+    reference's form.
     """
-    return (subscripts, tuple(tuple(op.shape) for op in operands), precision)
+    key = (subscripts, tuple(tuple(op.shape) for op in operands), precision)
+    return key if optimize == "greedy" else key + (optimize,)
 
 
 def clear_plan_cache() -> None:
@@ -128,18 +135,28 @@ def _backend_for(strategy: str, operands: tuple) -> str:
     return "hip" if (HAS_HIP and _use_hip()) else "pytorch"
 
 
-def plan_contraction(subscripts: str, *operands: torch.Tensor, precision: str = "fast") -> ContractionPlan:
+def plan_contraction(
+    subscripts: str, *operands: torch.Tensor, precision: str = "fast", optimize: str = "greedy"
+) -> ContractionPlan:
     """Validate, then return the (cached) plan for this subscript/shape/precision.
 
     Validation runs on every call, before the cache lookup; an unknown
     ``precision`` raises ``ValueError``. Two operands get a binary strategy,
-    three or more a greedy path, one operand the "torch" label
+    three or more a path, one operand the "torch" label
     (reference trntensor/plan.py:140-185).
+
+    ``optimize`` picks the path search for 3+ operands: ``"greedy"`` (default)
+    is the reference's rule, so ``contraction_path`` matches the reference;
+    ``"optimal"`` returns the order with the fewest total multiply-adds under
+    the same per-step cost (see ``_optimal_path_search``). It changes only the
+    order of pairwise steps, never the result beyond rounding.
     """
     _validate_subscripts(subscripts, operands)
     if precision not in ("fast", "kahan", "dd"):
         raise ValueError(f"precision must be 'fast', 'kahan', or 'dd', got {precision!r}")
-    key = _shape_key(subscripts, operands, precision)
+    if optimize not in PATH_SEARCHES:
+        raise ValueError(f"optimize must be one of {PATH_SEARCHES}, got {optimize!r}")
+    key = _shape_key(subscripts, operands, precision, optimize)
     hit = _PLAN_CACHE.get(key)
     if hit is not None:
         return hit
@@ -152,10 +169,11 @@ def plan_contraction(subscripts: str, *operands: torch.Tensor, precision: str = 
         extents: dict[str, int] = {}
         for term, op in zip(terms, operands):
             extents.update((c, int(n)) for c, n in zip(term, op.shape))
+        search = _optimal_path_search if optimize == "optimal" else _greedy_path_search
         plan = ContractionPlan(
             subscripts=subscripts,
             strategy="path",
-            contraction_path=_greedy_path_search(terms, out, extents),
+            contraction_path=search(terms, out, extents),
         )
     else:
         plan = ContractionPlan(subscripts=subscripts, strategy="torch")
@@ -198,6 +216,132 @@ def _greedy_path_search(input_list: list[str], output_str: str, size_map: dict[s
                     inter = union & _survivors(terms, i, j, output_str)
                     best = (i, j, "".join(sorted(inter)))
         i, j, name = best
+        path.append((i, j))
+        terms = [t for k, t in enumerate(terms) if k != i and k != j] + [name]
+    path.append((0, 1))
+    return path
+
+
+def path_cost(input_list: list[str], output_str: str, size_map: dict[str, int], path: list[tuple[int, int]]) -> int:
+    """Total multiply-adds of a pairwise path under the greedy search's step
+    cost (product of the extents of every letter either operand carries).
+    Intermediates carry the letters that a later operand or the output needs."""
+    terms = list(input_list)
+    total = 0
+    for i, j in path:
+        union = set(terms[i]) | set(terms[j])
+        cost = 1
+        for letter in union:
+            cost *= size_map.get(letter, 1)
+        total += cost
+        name = "".join(sorted(union & _survivors(terms, i, j, output_str)))
+        terms = [t for k, t in enumerate(terms) if k != i and k != j] + [name]
+    return total
+
+
+OPTIMAL_MAX_OPERANDS = 10
+
+
+def _optimal_path_search(input_list: list[str], output_str: str, size_map: dict[str, int]) -> list[tuple[int, int]]:
+    """Pairwise order with the fewest total multiply-adds (opt-in; the
+    reference has only the greedy rule).
+
+    Dynamic programming over operand subsets: the intermediate of a subset S
+    carries the letters of S that an operand outside S or the output needs
+    (an input keeps its own letters); contracting S1 with S2 costs the product
+    of the extents of their letters, as in the greedy rule; best(S) is the
+    minimum over splits S = S1 + S2 of best(S1) + best(S2) + that cost. The
+    search is O(3^n), so above OPTIMAL_MAX_OPERANDS operands it returns the
+    cheaper of the reference greedy path and a greedy path that picks the pair
+    whose intermediate shrinks the working set most (ties: fewer
+    multiply-adds, then first pair). The returned path uses the reference's
+    convention: (i, j) index the current list, the result is appended, the
+    last step is (0, 1).
+    """
+    n = len(input_list)
+    if n > OPTIMAL_MAX_OPERANDS:
+        cands = [_greedy_path_search(input_list, output_str, size_map), _shrink_path_search(input_list, output_str, size_map)]
+        return min(cands, key=lambda p: path_cost(input_list, output_str, size_map, p))
+
+    full = (1 << n) - 1
+    letters = [set(t) for t in input_list]
+    out = set(output_str)
+    sub_letters: dict[int, set] = {}
+    for s in range(1, full + 1):
+        acc: set = set()
+        for k in range(n):
+            if s >> k & 1:
+                acc |= letters[k]
+        sub_letters[s] = acc
+
+    def carried(s: int) -> set:
+        if s & (s - 1) == 0:
+            return letters[s.bit_length() - 1]
+        rest = sub_letters[full & ~s] if s != full else set()
+        return sub_letters[s] & (rest | out)
+
+    inter = {s: carried(s) for s in range(1, full + 1)}
+    best: dict[int, tuple[int, int]] = {1 << k: (0, 0) for k in range(n)}
+    for s in sorted(range(1, full + 1), key=lambda x: bin(x).count("1")):
+        if s & (s - 1) == 0:
+            continue
+        low = s & -s
+        choice = None
+        sub = (s - 1) & s
+        while sub:
+            if sub & low:  # each split once: S1 holds the lowest operand
+                other = s ^ sub
+                cost = 1
+                for letter in inter[sub] | inter[other]:
+                    cost *= size_map.get(letter, 1)
+                total = best[sub][0] + best[other][0] + cost
+                if choice is None or total < choice[0] or (total == choice[0] and sub < choice[1]):
+                    choice = (total, sub)
+            sub = (sub - 1) & s
+        best[s] = choice
+
+    cur = [1 << k for k in range(n)]
+    path: list[tuple[int, int]] = []
+
+    def emit(s: int) -> None:
+        if s & (s - 1) == 0:
+            return
+        s1 = best[s][1]
+        s2 = s ^ s1
+        emit(s1)
+        emit(s2)
+        i, j = sorted((cur.index(s1), cur.index(s2)))
+        path.append((i, j))
+        del cur[j], cur[i]
+        cur.append(s)
+
+    emit(full)
+    return path
+
+
+def _shrink_path_search(input_list: list[str], output_str: str, size_map: dict[str, int]) -> list[tuple[int, int]]:
+    """Greedy order by working-set size: each step takes the pair minimising
+    size(intermediate) - size(a) - size(b), ties by step multiply-adds, then
+    first pair (i < j scan)."""
+
+    def size(letters) -> int:
+        v = 1
+        for c in letters:
+            v *= size_map.get(c, 1)
+        return v
+
+    terms = list(input_list)
+    path: list[tuple[int, int]] = []
+    while len(terms) > 2:
+        best = None
+        for i in range(len(terms) - 1):
+            for j in range(i + 1, len(terms)):
+                union = set(terms[i]) | set(terms[j])
+                inter = union & _survivors(terms, i, j, output_str)
+                score = (size(inter) - size(terms[i]) - size(terms[j]), size(union))
+                if best is None or score < best[0]:
+                    best = (score, i, j, "".join(sorted(inter)))
+        _, i, j, name = best
         path.append((i, j))
         terms = [t for k, t in enumerate(terms) if k != i and k != j] + [name]
     path.append((0, 1))
