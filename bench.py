@@ -268,6 +268,18 @@ def bench_c2(torch, tt, dev, args):
                 "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK[key], 4),
             }
             del A, B, C
+    # precision="dd": double-double on the vector ALUs. Dot2 costs 10
+    # double-precision VALU operations per multiply-add; the ceiling is the
+    # fp64 vector rate, 78.6 TFLOP/s = 39.3e12 operations/s.
+    print("bench: c2 gemm4096 dd", file=sys.stderr, flush=True)
+    A, B = (torch.randn(4096, 4096, generator=g, dtype=torch.float64).to(dev) for _ in range(2))
+    wall, ev_ms = timed(torch, lambda: tt.einsum("ij,jk->ik", A, B, precision="dd"), 3, 1)
+    mac = 4096**3
+    out["gemm4096_dd"] = {
+        "ms": round(ev_ms, 3),
+        "TMAC/s": round(mac / (ev_ms * 1e-3) / 1e12, 3),
+        "frac_valu": round(10 * mac / (ev_ms * 1e-3) / 39.3e12, 4),
+    }
     return out
 
 

@@ -14,7 +14,10 @@
  *    memory and keeps no mutable global state, so calls are re-entrant.
  *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
  *    Work is enqueued on it and the call returns without synchronising.
- *  - dtype codes: TT_F32 = 0 (float), TT_F64 = 1 (double).
+ *  - dtype codes: TT_F32 = 0 (float), TT_F64 = 1 (double). TT_F64_DD = 2
+ *    (tt_gemm, tt_strided_contract only): double data, every product formed
+ *    exactly and summed in double-double (Ogita-Rump-Oishi Dot2), rounded
+ *    to double once per output.
  *  - Return codes: TT_OK 0; TT_INVALID 1 (bad argument: the Python layer
  *    raises ValueError); TT_UNSUPPORTED 2 (dtype/shape the kernels do not
  *    cover: NotImplementedError); TT_HIP_ERROR 3 (launch failure:
@@ -31,11 +34,11 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 1
+#define TT_ABI_VERSION 2
 #define TT_MAX_DIMS 8
 
 enum { TT_OK = 0, TT_INVALID = 1, TT_UNSUPPORTED = 2, TT_HIP_ERROR = 3 };
-enum { TT_F32 = 0, TT_F64 = 1 };
+enum { TT_F32 = 0, TT_F64 = 1, TT_F64_DD = 2 };
 
 /* ABI version of the loaded library (TT_ABI_VERSION at build time). */
 int tt_abi_version(void);
@@ -60,6 +63,11 @@ const char* tt_last_error(void);
  * (_kernels.py:77-117) behind nki_batched_matmul (dispatch.py:339-387), and
  * additionally folds einsum's alpha/beta epilogue (trntensor/einsum.py:99-102)
  * into the store. No padding: edge tiles are masked in the kernel.
+ *
+ * dtype TT_F64_DD runs a double-double GEMM on the vector ALUs (no MFMA):
+ * D = alpha * round(sum_k in double-double) (+ beta * C). It is the kernel
+ * behind precision="dd", which the reference declares but rejects with
+ * NotImplementedError (trntensor/einsum.py:112-116, plan.py:155).
  */
 int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
             double alpha, const void* A, int64_t lda, int64_t strideA,
@@ -157,7 +165,8 @@ size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, const int64_t* 
  * (n_red <= 8 dims); offsets are dot products of the multi-index with the
  * given element strides (0 broadcasts). B may be NULL (single operand:
  * the factor is 1). D and C are contiguous in out_shape order; C is read iff
- * non-NULL. Accumulation is in `dtype`.
+ * non-NULL. Accumulation is in `dtype`; TT_F64_DD accumulates double data
+ * in double-double (partial sums travel as pairs) and rounds once.
  *
  * No counterpart kernel in the reference: these contractions are the
  * "torch" strategy, which the reference hands to torch.einsum

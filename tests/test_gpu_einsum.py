@@ -150,9 +150,14 @@ class TestAlphaBetaDtypePrecision:
         assert kahan.dtype == torch.float32
         assert abs(float(kahan) - float(ref)) <= abs(float(fast) - float(ref)) + 1e-3
 
-    def test_dd_raises(self, hip):
-        with pytest.raises(NotImplementedError, match="kahan"):
-            trntensor.einsum("ij,jk->ik", torch.randn(4, 3), torch.randn(3, 5), precision="dd")
+    def test_dd_computes(self, hip):
+        """The reference raises NotImplementedError for precision='dd'
+        (tests/test_einsum.py:328-333); this build computes it (double-double
+        accumulation, tests/test_gpu_dd.py) and returns the first operand's dtype."""
+        A, B = torch.randn(4, 3), torch.randn(3, 5)
+        got = trntensor.einsum("ij,jk->ik", A, B, precision="dd")
+        assert got.dtype == torch.float32 and got.device.type == "cpu"
+        close(got, (A.double() @ B.double()).float())
 
     def test_fast_equals_default(self, hip):
         torch.manual_seed(0)

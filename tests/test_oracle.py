@@ -207,3 +207,45 @@ def test_multi_einsum_is_a_loop_of_einsum():
     np.testing.assert_allclose(r[0].numpy(), brute.einsum_f64("ij,jk->ik", A, B), rtol=1e-13)
     np.testing.assert_allclose(r[1].numpy(), brute.einsum_f64("ij,jk,kl->il", A, B, C), rtol=1e-12)
     np.testing.assert_allclose(float(r[2]), float(brute.einsum_f64("ij,ij->", A, A)), rtol=1e-13)
+
+
+class TestExactEinsum:
+    """Pins of oracle/brute.einsum_exact and ill_conditioned_dot (the dd oracle)."""
+
+    def test_matches_float64_on_easy_data(self):
+        g = torch.Generator().manual_seed(0)
+        A, B = torch.randn(7, 9, generator=g, dtype=torch.float64), torch.randn(9, 5, generator=g, dtype=torch.float64)
+        exact, scale, n = brute.einsum_exact("ij,jk->ik", A.numpy(), B.numpy())
+        assert n == 9
+        np.testing.assert_allclose(exact, (A @ B).numpy(), rtol=1e-14, atol=1e-14)
+        np.testing.assert_allclose(scale, (A.abs() @ B.abs()).numpy(), rtol=1e-14)
+
+    def test_closed_forms(self):
+        # cancellation float64 cannot see
+        r, _, _ = brute.einsum_exact("i->", np.array([1e16, 1.0, -1e16, 1.0]))
+        assert float(r) == 2.0
+        # one product is the correctly rounded float64 product
+        x, y = np.array([0.1]), np.array([0.3])
+        r, _, _ = brute.einsum_exact("i,i->", x, y)
+        assert float(r) == 0.1 * 0.3
+        # trace and outer product
+        M = np.arange(9.0).reshape(3, 3)
+        assert float(brute.einsum_exact("ii->", M)[0]) == 12.0
+        np.testing.assert_array_equal(brute.einsum_exact("i,j->ij", np.array([1.0, 2.0]), np.array([3.0]))[0], [[3.0], [6.0]])
+
+    def test_rounding_is_nearest(self):
+        # 1 + 2^-53 + 2^-80: exact sum rounds up to 1 + 2^-52 (above the tie)
+        r, _, _ = brute.einsum_exact("i->", np.array([1.0, 2.0**-53, 2.0**-80]))
+        assert float(r) == 1.0 + 2.0**-52
+        r, _, _ = brute.einsum_exact("i->", np.array([1.0, 2.0**-53]))  # tie: to even
+        assert float(r) == 1.0
+
+    def test_ill_conditioned_generator(self):
+        from fractions import Fraction
+
+        rng = np.random.default_rng(5)
+        for logc in (12, 20, 28):
+            x, y = brute.ill_conditioned_dot(200, logc, rng)
+            exact = sum((Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x, y)), Fraction(0))
+            cond = 2 * float(np.sum(np.abs(x * y))) / abs(float(exact))
+            assert 10 ** (logc - 3) <= cond <= 10 ** (logc + 4), (logc, cond)

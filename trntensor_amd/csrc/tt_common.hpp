@@ -87,6 +87,56 @@ __device__ __forceinline__ double block256_sum(double v, double* scratch) {
 }
 
 // ---------------------------------------------------------------------------
+// Double-double accumulation, after Ogita, Rump & Oishi, "Accurate sum and
+// dot product", SIAM J. Sci. Comput. 26(6), 2005: TwoSum (Knuth) and
+// TwoProduct (one FMA) are error-free transformations; Dot2 keeps the
+// running sum p and the sum s of every rounding error, so p + s is the dot
+// product as if accumulated in twice the working precision and rounded once.
+// Contraction into FMAs is switched off inside these helpers: fusing the
+// separate product into a following sum would change the values the error
+// terms are computed from.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void two_sum(double a, double b, double& sum, double& err) {
+#pragma clang fp contract(off)
+    const double s = a + b;
+    const double z = s - a;
+    err = (a - (s - z)) + (b - z);
+    sum = s;
+}
+
+struct Dot2 {
+    double p = 0.0, s = 0.0;
+
+    // p + s += a * b
+    __device__ __forceinline__ void add_prod(double a, double b) {
+#pragma clang fp contract(off)
+        const double h = a * b;
+        const double r = __builtin_fma(a, b, -h);
+        double np, q;
+        two_sum(p, h, np, q);
+        p = np;
+        s = s + (q + r);
+    }
+    // p + s += x
+    __device__ __forceinline__ void add(double x) {
+#pragma clang fp contract(off)
+        double np, q;
+        two_sum(p, x, np, q);
+        p = np;
+        s = s + q;
+    }
+    // p + s += o.p + o.s
+    __device__ __forceinline__ void merge(double op, double os) {
+#pragma clang fp contract(off)
+        double np, q;
+        two_sum(p, op, np, q);
+        p = np;
+        s = s + (q + os);
+    }
+    __device__ __forceinline__ double value() const { return p + s; }
+};
+
+// ---------------------------------------------------------------------------
 // XCD-aware workgroup order. The dispatcher hands workgroup w to XCD w % 8,
 // so consecutive ids land on different L2s. This maps the hardware id to a
 // logical id such that each XCD walks a contiguous range of logical ids

@@ -30,6 +30,8 @@ struct GemmArgs {
 
 // tt_gemm after argument checks (store epilogue).
 int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
+// Double-double GEMM (dtype TT_F64_DD) on the vector ALUs; same arguments.
+int gemm_dd_dispatch(bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // Dot epilogue; writes one double per workgroup to g.partial and returns the
 // number of workgroups in *nparts.
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);

@@ -47,15 +47,72 @@ struct StridedArgs {
     double alpha, beta;
 };
 
+// Accumulator of one output: plain sum in T, or double-double (Dot2) for
+// TT_F64_DD, whose partial sums travel as (p, s) pairs.
+template <typename T, bool DD>
+struct Acc;
+
 template <typename T>
-__device__ __forceinline__ T finish(const StridedArgs& g, int64_t o, T acc) {
-    T v = acc;
+struct Acc<T, false> {
+    T v = T(0);
+    __device__ __forceinline__ void add_prod(T x, T y) { v += x * y; }
+    __device__ __forceinline__ void add(T x) { v += x; }
+    __device__ __forceinline__ void wave_reduce() {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    }
+    __device__ __forceinline__ void put(double* red, int w) const { red[w] = (double)v; }
+    // Four wave totals in a fixed order.
+    __device__ __forceinline__ void take4(const double* red) { v = ((T)red[0] + (T)red[1]) + ((T)red[2] + (T)red[3]); }
+    __device__ __forceinline__ void store_partial(void* P, int64_t idx, int64_t plane) const {
+        (void)plane;
+        static_cast<T*>(P)[idx] = v;
+    }
+    __device__ __forceinline__ void add_partial(const void* P, int64_t idx, int64_t plane) {
+        (void)plane;
+        v += static_cast<const T*>(P)[idx];
+    }
+    __device__ __forceinline__ T value() const { return v; }
+};
+
+template <>
+struct Acc<double, true> : Dot2 {
+    __device__ __forceinline__ void wave_reduce() {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const double op = __shfl_xor(p, off, 64);
+            const double os = __shfl_xor(s, off, 64);
+            merge(op, os);
+        }
+    }
+    __device__ __forceinline__ void put(double* red, int w) const {
+        red[w] = p;
+        red[4 + w] = s;
+    }
+    __device__ __forceinline__ void take4(const double* red) {
+        p = red[0];
+        s = red[4];
+        for (int w = 1; w < 4; ++w) merge(red[w], red[4 + w]);
+    }
+    // p in plane 0, s in plane 1 (plane = nsplit * n_out doubles).
+    __device__ __forceinline__ void store_partial(void* P, int64_t idx, int64_t plane) const {
+        static_cast<double*>(P)[idx] = p;
+        static_cast<double*>(P)[plane + idx] = s;
+    }
+    __device__ __forceinline__ void add_partial(const void* P, int64_t idx, int64_t plane) {
+        merge(static_cast<const double*>(P)[idx], static_cast<const double*>(P)[plane + idx]);
+    }
+};
+
+template <typename T, bool DD>
+__device__ __forceinline__ T finish(const StridedArgs& g, int64_t o, const Acc<T, DD>& acc) {
+    T v = acc.value();
     if (g.alpha != 1.0) v = (T)g.alpha * v;
     if (g.C) v = v + (T)g.beta * static_cast<const T*>(g.C)[o];
     return v;
 }
 
-template <typename T>
+template <typename T, bool DD>
 __global__ __launch_bounds__(256) void strided_per_output_kernel(StridedArgs g) {
     const T* A = static_cast<const T*>(g.A);
     const T* B = static_cast<const T*>(g.B);
@@ -63,63 +120,62 @@ __global__ __launch_bounds__(256) void strided_per_output_kernel(StridedArgs g) 
     for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < g.n_out; o += (int64_t)gridDim.x * 256) {
         int64_t oa, ob;
         decode((uint32_t)o, g.out, oa, ob);
-        T acc = T(0);
+        Acc<T, DD> acc;
         for (int64_t r = 0; r < g.n_red; ++r) {
             int64_t ra, rb;
             decode((uint32_t)r, g.red, ra, rb);
             const T x = A[oa + ra];
-            acc += B ? x * B[ob + rb] : x;
+            if (B) acc.add_prod(x, B[ob + rb]);
+            else acc.add(x);
         }
-        D[o] = finish<T>(g, o, acc);
+        D[o] = finish<T, DD>(g, o, acc);
     }
 }
 
 // Grid: (n_out, nsplit). Workgroup (o, s) reduces r = s*256 + t + k*nsplit*256.
-template <typename T>
+template <typename T, bool DD>
 __global__ __launch_bounds__(256) void strided_per_block_kernel(StridedArgs g) {
-    __shared__ double red[4];
+    __shared__ double red[8];
     const T* A = static_cast<const T*>(g.A);
     const T* B = static_cast<const T*>(g.B);
     const int64_t o = blockIdx.x;
     const int64_t s = blockIdx.y;
     int64_t oa, ob;
     decode((uint32_t)o, g.out, oa, ob);
-    T acc = T(0);
+    Acc<T, DD> acc;
     const int64_t step = g.nsplit * 256;
     for (int64_t r = s * 256 + threadIdx.x; r < g.n_red; r += step) {
         int64_t ra, rb;
         decode((uint32_t)r, g.red, ra, rb);
         const T x = A[oa + ra];
-        acc += B ? x * B[ob + rb] : x;
+        if (B) acc.add_prod(x, B[ob + rb]);
+        else acc.add(x);
     }
-    // Block sum in T: wavefront shuffles then four wave totals.
-    T v = acc;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
+    // Block sum: wavefront shuffles, then the four wave totals in order.
+    acc.wave_reduce();
+    if ((threadIdx.x & 63) == 0) acc.put(red, threadIdx.x >> 6);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const T tot = ((T)red[0] + (T)red[1]) + ((T)red[2] + (T)red[3]);
-        if (g.nsplit == 1) static_cast<T*>(g.D)[o] = finish<T>(g, o, tot);
-        else static_cast<T*>(g.partial)[s * g.n_out + o] = tot;
+        Acc<T, DD> tot;
+        tot.take4(red);
+        if (g.nsplit == 1) static_cast<T*>(g.D)[o] = finish<T, DD>(g, o, tot);
+        else tot.store_partial(g.partial, s * g.n_out + o, g.nsplit * g.n_out);
     }
 }
 
-template <typename T>
+template <typename T, bool DD>
 __global__ __launch_bounds__(256) void strided_finish_kernel(StridedArgs g) {
-    __shared__ double red[4];
+    __shared__ double red[8];
     const int64_t o = blockIdx.x;
-    const T* P = static_cast<const T*>(g.partial);
-    T acc = T(0);
-    for (int64_t s = threadIdx.x; s < g.nsplit; s += 256) acc += P[s * g.n_out + o];
-    T v = acc;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
+    Acc<T, DD> acc;
+    for (int64_t s = threadIdx.x; s < g.nsplit; s += 256) acc.add_partial(g.partial, s * g.n_out + o, g.nsplit * g.n_out);
+    acc.wave_reduce();
+    if ((threadIdx.x & 63) == 0) acc.put(red, threadIdx.x >> 6);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const T tot = ((T)red[0] + (T)red[1]) + ((T)red[2] + (T)red[3]);
-        static_cast<T*>(g.D)[o] = finish<T>(g, o, tot);
+        Acc<T, DD> tot;
+        tot.take4(red);
+        static_cast<T*>(g.D)[o] = finish<T, DD>(g, o, tot);
     }
 }
 
@@ -149,17 +205,17 @@ static int64_t prod(int n, const int64_t* s) {
     return r;
 }
 
-template <typename T>
+template <typename T, bool DD>
 static int run_typed(StridedArgs g, int n_out_dims, const int64_t* out_shape, hipStream_t st) {
     const Plan pl = choose(g.n_out, g.n_red);
     g.nsplit = pl.nsplit;
     if (!pl.per_block) {
         int64_t blocks = (g.n_out + 255) / 256;
         if (blocks > 1 << 20) blocks = 1 << 20;
-        if (blocks > 0) hipLaunchKernelGGL(strided_per_output_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+        if (blocks > 0) hipLaunchKernelGGL((strided_per_output_kernel<T, DD>), dim3((unsigned)blocks), dim3(256), 0, st, g);
     } else {
-        hipLaunchKernelGGL(strided_per_block_kernel<T>, dim3((unsigned)g.n_out, (unsigned)g.nsplit), dim3(256), 0, st, g);
-        if (g.nsplit > 1) hipLaunchKernelGGL(strided_finish_kernel<T>, dim3((unsigned)g.n_out), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((strided_per_block_kernel<T, DD>), dim3((unsigned)g.n_out, (unsigned)g.nsplit), dim3(256), 0, st, g);
+        if (g.nsplit > 1) hipLaunchKernelGGL((strided_finish_kernel<T, DD>), dim3((unsigned)g.n_out), dim3(256), 0, st, g);
     }
     (void)n_out_dims;
     (void)out_shape;
@@ -175,7 +231,8 @@ extern "C" size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, cons
     const int64_t no = prod(n_out, out_shape), nr = prod(n_red, red_shape);
     const Plan p = choose(no, nr);
     if (!p.per_block || p.nsplit == 1) return 0;
-    const size_t es = dtype == TT_F64 ? 8 : 4;
+    // TT_F64_DD partials are (p, s) pairs of doubles.
+    const size_t es = dtype == TT_F64_DD ? 16 : dtype == TT_F64 ? 8 : 4;
     return ((size_t)(p.nsplit * no) * es + 255) / 256 * 256;
 }
 
@@ -187,8 +244,8 @@ extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shap
     using namespace tt;
     if (n_out < 0 || n_red < 0 || n_out > TT_MAX_DIMS || n_red > TT_MAX_DIMS)
         return set_error(TT_INVALID, "tt_strided_contract: dims out=%d red=%d (max %d)", n_out, n_red, TT_MAX_DIMS);
-    if (dtype != TT_F32 && dtype != TT_F64)
-        return set_error(TT_UNSUPPORTED, "tt_strided_contract: dtype %d (only TT_F32, TT_F64)", dtype);
+    if (dtype != TT_F32 && dtype != TT_F64 && dtype != TT_F64_DD)
+        return set_error(TT_UNSUPPORTED, "tt_strided_contract: dtype %d (only TT_F32, TT_F64, TT_F64_DD)", dtype);
     for (int k = 0; k < n_out; ++k)
         if (out_shape[k] < 0) return set_error(TT_INVALID, "tt_strided_contract: negative output extent");
     for (int k = 0; k < n_red; ++k)
@@ -230,6 +287,7 @@ extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shap
         // Empty reduction: every output is alpha * 0 (+ beta * C).
         g.n_red = 0;
     }
-    if (dtype == TT_F64) return run_typed<double>(g, n_out, out_shape, st);
-    return run_typed<float>(g, n_out, out_shape, st);
+    if (dtype == TT_F64_DD) return run_typed<double, true>(g, n_out, out_shape, st);
+    if (dtype == TT_F64) return run_typed<double, false>(g, n_out, out_shape, st);
+    return run_typed<float, false>(g, n_out, out_shape, st);
 }

@@ -54,7 +54,9 @@ def einsum(
     written; the result is a new tensor, as in the reference). ``dtype`` casts
     every operand first and the result comes back in that dtype.
     ``precision="kahan"`` contracts in float64 and returns the first operand's
-    dtype; ``"dd"`` raises ``NotImplementedError``. The result lives on the
+    dtype; ``"dd"`` forms every product exactly and sums in double-double,
+    rounding once per pairwise step (the reference raises
+    ``NotImplementedError`` for it). The result lives on the
     first operand's device: CPU operands are staged through the GPU.
     ``optimize`` selects the path search for 3+ operands: ``"greedy"`` (the
     reference's order, default) or ``"optimal"`` (fewest multiply-adds; opt-in).
@@ -84,16 +86,20 @@ def _execute_contraction(
 ) -> torch.Tensor:
     """Run a plan (reference trntensor/einsum.py:106-126).
 
-    "kahan" contracts in float64 and casts back to the first operand's dtype;
-    "dd" raises. Otherwise the strategy selects the executor: matmul and bmm
-    go to the GEMM core, "torch" to the general engine, "path" to the
-    pairwise executor.
+    "kahan" contracts in float64 and casts back to the first operand's dtype.
+    "dd" (which the reference rejects with NotImplementedError) contracts
+    float64 copies with every product exact and every sum in double-double,
+    rounded to float64 once per pairwise step, then casts back. Otherwise
+    the strategy selects the executor: matmul and bmm go to the GEMM core,
+    "torch" to the general engine, "path" to the pairwise executor.
     """
     if plan.precision == "dd":
-        raise NotImplementedError(
-            "precision='dd' (double-double accumulation) has no kernel yet; "
-            "use precision='kahan' (fp64 accumulation) as an alternative."
-        )
+        with engine.accumulation("dd"):
+            return _run(subscripts, operands, plan, alpha, beta, out, torch.float64)
+    return _run(subscripts, operands, plan, alpha, beta, out, None)
+
+
+def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
     dispatch.require_hip()
     devs, orig = dispatch.place(*operands, *([out] if out is not None else []))
     ops = devs[: len(operands)]
@@ -102,7 +108,7 @@ def _execute_contraction(
     if len(dts) > 1:
         raise RuntimeError(f"einsum(): operands must share one dtype, got {sorted(str(d) for d in dts)}")
     res_dtype = ops[0].dtype
-    cd = torch.float64 if plan.precision == "kahan" else dispatch.compute_dtype(res_dtype)
+    cd = cd_override or (torch.float64 if plan.precision == "kahan" else dispatch.compute_dtype(res_dtype))
     ops = [o.to(cd) for o in ops]
     lhs, out_str = _parse_subscripts(subscripts)
     terms = lhs.split(",")
@@ -248,7 +254,8 @@ def _execute_path(
     outer product of 'ia,jb,abP,ijP->' are never written.
     """
     names = _path_names(terms, out, path)
-    plan = _fusion_plan(terms, out, path, names)
+    # The fused dot epilogue accumulates in float64 only.
+    plan = None if engine._ACCUMULATION.get() == "dd" else _fusion_plan(terms, out, path, names)
     deferred = set() if plan is None else {s for s in plan if s is not None}
     cur_terms = list(terms)
     cur: list = list(ops)

@@ -25,6 +25,8 @@ defines them.
 
 from __future__ import annotations
 
+import contextlib
+import contextvars
 import ctypes
 
 import torch
@@ -33,11 +35,29 @@ from . import _lib
 
 _MAX_INDEX = (1 << 31) - 1
 
+# Accumulation of float64 launches: "native" (float64) or "dd" (double-double,
+# dtype code TT_F64_DD). Set for a block of calls with `accumulation(...)`.
+_ACCUMULATION: contextvars.ContextVar[str] = contextvars.ContextVar("tt_accumulation", default="native")
+
+
+@contextlib.contextmanager
+def accumulation(mode: str):
+    """Run the enclosed float64 launches with `mode` accumulation ("native" | "dd")."""
+    if mode not in ("native", "dd"):
+        raise ValueError(f"accumulation mode {mode!r}")
+    token = _ACCUMULATION.set(mode)
+    try:
+        yield
+    finally:
+        _ACCUMULATION.reset(token)
+
 
 def dtype_code(dt: torch.dtype) -> int:
     if dt == torch.float64:
-        return _lib.TT_F64
+        return _lib.TT_F64_DD if _ACCUMULATION.get() == "dd" else _lib.TT_F64
     if dt == torch.float32:
+        if _ACCUMULATION.get() == "dd":
+            raise NotImplementedError("double-double accumulation needs float64 data")
         return _lib.TT_F32
     raise NotImplementedError(f"HIP kernels compute in float32/float64, not {dt}")
 
@@ -347,7 +367,8 @@ class _GemmRecipe:
     def run(self, At, Bt, alpha, beta, C):
         D = torch.empty(self.shape, dtype=self.dt, device=At.device)
         X, Y = (Bt, At) if self.swap else (At, Bt)
-        if self.split <= 1:
+        # K-slices would each round to float64: double-double runs unsplit.
+        if self.split <= 1 or _ACCUMULATION.get() == "dd":
             gemm(self.ta, self.tb, self.M, self.N, self.K, X, self.lda, self.sA, Y, self.ldb, self.sB, D,
                  self.ldd, self.sD, self.batch, alpha, beta, C, self.ldd, self.sD)
             return D
@@ -584,7 +605,11 @@ def contract(
         batch = [c for c in out if c in la and c in lb]
         ml = [c for c in out if c in la and c not in lb]
         nl = [c for c in out if c in lb and c not in la]
-        if kl:
+        # Under double-double accumulation a pre-reduced operand would be
+        # rounded to float64 before the GEMM; such contractions take the
+        # strided kernel, which accumulates the whole reduction in one pair.
+        one_sided = any(c not in lb and c not in lo for c in la) or any(c not in la and c not in lo for c in lb)
+        if kl and not (one_sided and _ACCUMULATION.get() == "dd"):
             M = _numel(ext[c] for c in ml)
             N = _numel(ext[c] for c in nl)
             if prefer_gemm or (M >= 16 and N >= 16):
