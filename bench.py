@@ -34,7 +34,9 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # The GPU ramps its clocks over the first ~0.1-0.2 s of work after idle;
+    # 25 warm-up steps (~0.2 s) put the timed steps in steady state.
+    ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5)")
@@ -65,6 +67,19 @@ def timed(torch, fn, steps, warmup):
     return wall, ev
 
 
+def timed_steady(torch, fn, steps, min_warm_s=0.3):
+    """timed() after warming up for at least `min_warm_s` seconds of work (the
+    secondary configs follow host-side input generation, during which the GPU
+    idles and its clocks drop)."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < 2 or time.perf_counter() - t0 < min_warm_s:
+        fn()
+        torch.cuda.synchronize()
+        n += 1
+    return timed(torch, fn, steps, 0)
+
+
 def mp2_inputs(torch, dtype, nocc=64, nvir=320, naux=1200):
     g = torch.Generator().manual_seed(0)
     B = torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64) * 0.05
@@ -81,6 +96,27 @@ def traffic_from_profiles(kernel_key):
             return json.load(f).get(kernel_key)
     except (OSError, ValueError):
         return None
+
+
+def cpu_threads(torch):
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    return threads
+
+
+def cpu_timed(torch, fn, reps=2):
+    """Host wall seconds per call of the reference CPU path: one warm-up, then
+    the mean of `reps` calls."""
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def cpu_entry(torch, seconds, flop, sample, threads):
+    return {"ms": round(seconds * 1e3, 3), "GFLOP/s": round(flop / seconds / 1e9, 2), "cores": threads,
+            "kind": "port", "sample": sample}
 
 
 def cpu_mp2_baseline(torch, seconds=12.0):
@@ -147,6 +183,8 @@ def main():
             extra["c4_mp2_fp32"] = bench_c4_f32(torch, tt, dev, args)
         if "c2" in want:
             extra["c2"] = bench_c2(torch, tt, dev, args)
+        if "c1" in want:
+            extra["c1_einsum_loop_fp32"] = bench_c1(torch, tt, dev, args)
         if "c5" in want:
             extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
         print(json.dumps({"configs": extra}))
@@ -221,12 +259,23 @@ def bench_c3(torch, tt, dev, args):
     C = torch.linalg.qr(torch.randn(512, 64, generator=g, dtype=torch.float64))[0].contiguous().to(dev)
     eri = torch.randn(512, 512, 1536, generator=g, dtype=torch.float64).to(dev)
     eri = ((eri + eri.permute(1, 0, 2)) * (0.05 / 2**0.5)).contiguous()
-    wall, ev_ms = timed(torch, lambda: tt.einsum("mi,mnP->inP", C, eri), max(5, args.steps), args.warmup)
+    wall, ev_ms = timed_steady(torch, lambda: tt.einsum("mi,mnP->inP", C, eri), max(5, args.steps))
     byt = (512 * 512 * 1536 + 64 * 512 * 1536 + 512 * 64) * 8
     flop = 2 * 64 * 512 * 512 * 1536
     t = ev_ms * 1e-3
     t_floor = max(flop / PEAK["f64"], byt / PEAK["hbm"])
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_ref
+
+        threads = cpu_threads(torch)
+        Cc, ec = C.cpu(), eri.cpu()
+        del eri
+        sec = cpu_timed(torch, lambda: cpu_ref.einsum("mi,mnP->inP", Cc, ec))
+        cpu = cpu_entry(torch, sec, flop, "full config 3 through the reference's 'torch' strategy (torch.einsum)", threads)
+        del Cc, ec
     return {
+        "cpu": cpu,
         "ms": round(ev_ms, 4),
         "wall_ms": round(wall, 4),
         "GB/s": round(byt / t / 1e9, 1),
@@ -242,9 +291,19 @@ def bench_c3(torch, tt, dev, args):
 def bench_c4_f32(torch, tt, dev, args):
     print("bench: c4 mp2 fp32", file=sys.stderr, flush=True)
     B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, torch.float32))
-    wall, ev_ms = timed(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps, args.warmup)
+    wall, ev_ms = timed_steady(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps)
     flop = 2080 * 2 * 320**2 * 1200
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cpu_ref
+
+        threads = cpu_threads(torch)
+        Bc, eoc, evc = B.cpu(), eo.cpu(), ev.cpu()
+        pairs = [(i, j) for i in range(64) for j in range(64)]
+        sec = cpu_timed(torch, lambda: cpu_ref.mp2_energy_pairs(Bc, eoc, evc, pairs[:256]), reps=1) * 16
+        cpu = cpu_entry(torch, sec, flop, "256 of 4096 ordered (i,j) pairs of the reference loop, scaled x16", threads)
     return {
+        "cpu": cpu,
         "ms": round(ev_ms, 4),
         "GFLOP/s": round(flop / (wall * 1e-3) / 1e9, 1),
         "frac_mfma_f32": round(flop / (ev_ms * 1e-3) / PEAK["f32"], 4),
@@ -260,20 +319,28 @@ def bench_c2(torch, tt, dev, args):
     ):
         for dt, key in ((torch.float64, "f64"), (torch.float32, "f32")):
             print(f"bench: c2 {name} {key}", file=sys.stderr, flush=True)
-            A, B, C = (torch.randn(*shape, generator=g, dtype=torch.float64).to(dev, dt) for _ in range(3))
-            wall, ev_ms = timed(torch, lambda: tt.einsum(sub, A, B, alpha=1.5, beta=0.5, out=C), max(5, args.steps), args.warmup)
+            hostA, hostB, hostC = (torch.randn(*shape, generator=g, dtype=torch.float64).to(dt) for _ in range(3))
+            A, B, C = (x.to(dev) for x in (hostA, hostB, hostC))
+            wall, ev_ms = timed_steady(torch, lambda: tt.einsum(sub, A, B, alpha=1.5, beta=0.5, out=C), max(5, args.steps))
             out[f"{name}_{key}"] = {
                 "ms": round(ev_ms, 4),
                 "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
                 "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK[key], 4),
             }
-            del A, B, C
+            if not args.no_cpu:
+                from oracle import cpu_ref
+
+                threads = cpu_threads(torch)
+                sec = cpu_timed(torch, lambda: cpu_ref.einsum(sub, hostA, hostB, alpha=1.5, beta=0.5, out=hostC))
+                out[f"{name}_{key}"]["cpu"] = cpu_entry(
+                    torch, sec, flop, "full config through the reference's matmul/bmm executor plus the alpha/beta passes", threads)
+            del A, B, C, hostA, hostB, hostC
     # precision="dd": double-double on the vector ALUs. Dot2 costs 10
     # double-precision VALU operations per multiply-add; the ceiling is the
     # fp64 vector rate, 78.6 TFLOP/s = 39.3e12 operations/s.
     print("bench: c2 gemm4096 dd", file=sys.stderr, flush=True)
     A, B = (torch.randn(4096, 4096, generator=g, dtype=torch.float64).to(dev) for _ in range(2))
-    wall, ev_ms = timed(torch, lambda: tt.einsum("ij,jk->ik", A, B, precision="dd"), 3, 1)
+    wall, ev_ms = timed_steady(torch, lambda: tt.einsum("ij,jk->ik", A, B, precision="dd"), 3)
     mac = 4096**3
     out["gemm4096_dd"] = {
         "ms": round(ev_ms, 3),
@@ -309,7 +376,15 @@ def bench_c1(torch, tt, dev, args):
     for _ in range(20):
         float(tt.mp2_energy(B, eo, ev))
     t_fused = (time.perf_counter() - t0) / 20
-    return {"einsum_loop_ms": round(t_loop * 1e3, 3), "fused_cpu_operands_ms": round(t_fused * 1e3, 3)}
+    res = {"einsum_loop_ms": round(t_loop * 1e3, 3), "fused_cpu_operands_ms": round(t_fused * 1e3, 3)}
+    if not args.no_cpu:
+        from oracle import cpu_ref
+
+        threads = cpu_threads(torch)
+        sec = cpu_timed(torch, lambda: cpu_ref.df_mp2_einsum_loop(B, eo, ev), reps=5)
+        res["cpu"] = {"einsum_loop_ms": round(sec * 1e3, 3), "cores": threads, "kind": "port",
+                      "sample": "the reference example loop (64 einsum calls) on the same CPU tensors"}
+    return res
 
 
 def bench_c5(torch, tt, dev, args):
@@ -319,14 +394,27 @@ def bench_c5(torch, tt, dev, args):
     B = (torch.randn(128, 400, generator=g, dtype=torch.float64) * 0.1).to(dev)
     W = (torch.randn(400, 400, 800, generator=g, dtype=torch.float64) * 0.01).to(dev)
     V = (torch.randn(128, 128, 800, generator=g, dtype=torch.float64) * 0.1).to(dev)
-    wall, ev_ms = timed(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V), 3, 1)
+    wall, ev_ms = timed_steady(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V), 3)
     flop = 2.62144e9 + 2 * 2.097152e12 + 2 * 2.62144e9
     res = {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2), "path": "reference greedy [(0,1),(0,1),(0,1)]"}
     # opt-in fewest-multiply-add order: 2*(1.6384e10 + 5.24288e9 + 51200) flop
-    wall, ev_ms = timed(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V, optimize="optimal"), 10, 2)
+    wall, ev_ms = timed_steady(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V, optimize="optimal"), 10)
     flop = 2 * (1.6384e10 + 5.24288e9 + 51200)
     res["optimize_optimal"] = {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
                                "path": "[(1,2),(1,2),(0,1)]", "speedup": round(res["ms"] / ev_ms, 1)}
+    if not args.no_cpu:
+        from oracle import cpu_ref
+
+        threads = cpu_threads(torch)
+        # Sample: a restricted to 40 of 400. The greedy path keeps its order
+        # ([(0,1),(0,1),(0,1)]: the first pair stays cheapest) and every
+        # step's work is linear in a, so the time scales by 10.
+        Ac, Bc, Wc, Vc = A[:, :40].cpu(), B.cpu(), W[:40].cpu(), V.cpu()
+        assert cpu_ref.plan_contraction("ia,jb,abP,ijP->", Ac, Bc, Wc, Vc).contraction_path == [(0, 1), (0, 1), (0, 1)]
+        sec = cpu_timed(torch, lambda: cpu_ref.einsum("ia,jb,abP,ijP->", Ac, Bc, Wc, Vc), reps=1) * 10
+        res["cpu"] = cpu_entry(torch, sec, 2.62144e9 + 2 * 2.097152e12 + 2 * 2.62144e9,
+                               "reference greedy path with a restricted to 40 of 400 (same path, work linear in a), x10",
+                               threads)
     return res
 
 
