@@ -84,6 +84,8 @@ def _check(terms, out, ops, alpha=1.0, beta=0.0, C=None, prefer_gemm=False):
         ("ijP,ajP->ia", dict(i=3, a=5, j=16, P=300)),  # K = 4800: split into 9 slices + remainder
         ("ijP,ajP->ai", dict(i=3, a=5, j=16, P=256)),  # K = 4096, swapped output, split
         ("ab,bc->ac", dict(a=1, b=5000, c=1)),  # GEMV-like, split
+        ("ab,bc->ac", dict(a=0, b=5000, c=3)),  # empty output, long K
+        ("ab,bc->ac", dict(a=4, b=0, c=3)),  # K = 0: beta * C only
     ],
 )
 def test_gemm_mappings(emulated, sub, ext):
@@ -116,6 +118,7 @@ def test_split_k_choice():
     assert engine.split_k(128, 128, 4095, 1) == 1  # short K
     assert engine.split_k(128, 128, 8192, 2) == 1  # batched
     assert engine.split_k(1, 1, 5000, 1) == 9
+    assert engine.split_k(0, 7, 8192, 1) == 1  # empty output
 
 
 def test_random_two_operand_contractions(emulated):
@@ -132,3 +135,63 @@ def test_random_two_operand_contractions(emulated):
         out = "".join(c for c in rng.sample(seen, len(seen)) if rng.random() < 0.5)
         ops = [_operand(ta, ext, gen, rng), _operand(tb, ext, gen, rng)]
         _check([ta, tb], out, ops, prefer_gemm=rng.random() < 0.5)
+
+
+def emu_gemm_dot(transA, transB, M, N, K, A, lda, sA, B, ldb, sB, batch, m_lo_extent, n_lo_extent, E1, e1s, E2, e2s,
+                 alpha, beta, C, out, a_off=0, b_off=0):
+    """tt_gemm_dot's contract (include/trntensor_hip.h): out = alpha sum X.*E (+ beta C[0]),
+    E(b,m,n) = E1[o(e1s)] * E2[o(e2s)], o(s) = m_hi s0 + m_lo s1 + n_hi s2 + n_lo s3 + b s4."""
+    opA = torch.as_strided(A, (batch, M, K), (sA, 1, lda) if transA else (sA, lda, 1), A.storage_offset() + a_off)
+    opB = torch.as_strided(B, (batch, K, N), (sB, 1, ldb) if transB else (sB, ldb, 1), B.storage_offset() + b_off)
+    X = torch.bmm(opA.double(), opB.double())
+    b = torch.arange(batch).view(-1, 1, 1)
+    m = torch.arange(M).view(1, -1, 1)
+    n = torch.arange(N).view(1, 1, -1)
+
+    def gather(E, s):
+        off = (m // m_lo_extent) * s[0] + (m % m_lo_extent) * s[1] + (n // n_lo_extent) * s[2] + (n % n_lo_extent) * s[3] + b * s[4]
+        return _flat(E)[off]
+
+    E = gather(E1, e1s)
+    if E2 is not None:
+        E = E * gather(E2, e2s)
+    v = alpha * float((X * E.double()).sum())
+    if C is not None:
+        v += beta * float(C.reshape(-1)[0])
+    out.fill_(v)
+
+
+def _flat(E):
+    """Element view of E's storage from its first element (strides are element offsets)."""
+    return torch.as_strided(E, (E.untyped_storage().nbytes() // E.element_size() - E.storage_offset(),), (1,), E.storage_offset())
+
+
+@pytest.mark.parametrize(
+    "gterms,xname,shapes,factors",
+    [
+        # config-5 shape: abP,ijP -> abij dotted with the outer product ia x jb
+        (["abP", "ijP"], "abij", [(5, 6, 7), (3, 4, 7)], [("ia", (3, 5)), ("jb", (4, 6))]),
+        # optimal-order shape with a long K: split into slices with E batch stride 0
+        (["ijP", "ajP"], "ia", [(3, 16, 300), (5, 16, 300)], [("ia", (3, 5))]),
+        # the same with row-contiguous operands (k-step = leading dimension)
+        (["jPi", "jPa"], "ia", [(16, 300, 3), (16, 300, 5)], [("ia", (3, 5))]),
+        # batch letter
+        (["bij", "bjk"], "bik", [(3, 7, 9), (3, 9, 5)], [("bik", (3, 7, 5))]),
+        # partner in another letter order than the product
+        (["ij", "jk"], "ik", [(6, 8), (8, 9)], [("ki", (9, 6))]),
+    ],
+)
+def test_gemm_dot_mappings(monkeypatch, gterms, xname, shapes, factors):
+    monkeypatch.setattr(engine, "gemm", emu_gemm)
+    monkeypatch.setattr(engine, "strided_contract", emu_strided)
+    monkeypatch.setattr(engine, "gemm_dot", emu_gemm_dot)
+    gen = torch.Generator().manual_seed(3)
+    tens = [torch.randn(*s, generator=gen, dtype=torch.float64) for s in shapes]
+    facs = [(t, torch.randn(*s, generator=gen, dtype=torch.float64)) for t, s in factors]
+    C = torch.tensor(0.75, dtype=torch.float64)
+    got = engine.contract_gemm_dot(gterms, xname, tens, facs, 1.5, 0.5, C)
+    assert got is not None
+    X = torch.einsum(",".join(gterms) + "->" + xname, *tens)
+    E = torch.einsum(",".join(t for t, _ in facs) + "->" + xname, *[f for _, f in facs])
+    want = 1.5 * float((X * E).sum()) + 0.5 * 0.75
+    assert abs(float(got) - want) <= 1e-12 * (1 + abs(want))

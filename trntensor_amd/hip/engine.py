@@ -332,7 +332,7 @@ def split_k(M: int, N: int, K: int, batch: int) -> int:
     batch entries gives ~512 workgroups. Only unbatched GEMMs with K >= 4096
     are split.
     """
-    if batch > 1 or K < 4096:
+    if batch > 1 or K < 4096 or M == 0 or N == 0:
         return 1
     tiles = (-(-M // 128)) * (-(-N // 128))
     if tiles >= 192:
@@ -343,6 +343,49 @@ def split_k(M: int, N: int, K: int, batch: int) -> int:
 def _k_step(k_contiguous: bool, ld: int) -> int:
     """Element distance between consecutive k of an operand viewed rows x K."""
     return 1 if k_contiguous else ld
+
+
+def gemm_dot(
+    transA: bool,
+    transB: bool,
+    M: int,
+    N: int,
+    K: int,
+    A: torch.Tensor,
+    lda: int,
+    sA: int,
+    B: torch.Tensor,
+    ldb: int,
+    sB: int,
+    batch: int,
+    m_lo_extent: int,
+    n_lo_extent: int,
+    E1: torch.Tensor,
+    e1_strides: list[int],
+    E2: torch.Tensor | None,
+    e2_strides: list[int] | None,
+    alpha: float,
+    beta: float,
+    C: torch.Tensor | None,
+    out: torch.Tensor,
+    a_off: int = 0,
+    b_off: int = 0,
+) -> None:
+    """tt_gemm_dot on torch tensors: out = alpha * sum (op(A) op(B)) .* E (+ beta * C[0])."""
+    lib = _lib.load()
+    code = dtype_code(A.dtype)
+    es = A.element_size()
+    wsb = lib.tt_gemm_dot_workspace_bytes(code, M, N, batch)
+    ws = _workspace(wsb, A.device)
+    st = lib.tt_gemm_dot(
+        code, int(transA), int(transB), M, N, K,
+        ctypes.c_void_p(A.data_ptr() + a_off * es), lda, sA,
+        ctypes.c_void_p(B.data_ptr() + b_off * es), ldb, sB, batch,
+        m_lo_extent, n_lo_extent,
+        _ptr(E1), _lib.i64_array(e1_strides), _ptr(E2), None if E2 is None else _lib.i64_array(e2_strides),
+        float(alpha), float(beta), _ptr(C), _ptr(out), _ptr(ws), wsb, _stream_ptr(A.device),
+    )
+    _lib.check(st, "tt_gemm_dot")
 
 
 class _GemmRecipe:
@@ -689,7 +732,7 @@ def contract_gemm_dot(
     if set().union(*[set(f.letters) for f in facs]) != lo or len(xname) != len(lo):
         return None
     dt, dev = A.t.dtype, A.t.device
-    code = dtype_code(dt)
+    dtype_code(dt)  # raises for dtypes the kernels do not compute in
     for idx, (op, other) in enumerate(((A, lb), (B, la))):
         gone = [c for c in op.letters if c not in other and c not in lo]
         if gone:
@@ -724,26 +767,18 @@ def contract_gemm_dot(
     b_l = batch[0] if batch and nb > 1 else None  # K-slices reuse the batch index with E stride 0
 
     def strides(f: Operand):
-        return _lib.i64_array([0 if c is None else f.strd.get(c, 0) for c in (m_hi, m_lo, n_hi, n_lo, b_l)])
+        return [0 if c is None else f.strd.get(c, 0) for c in (m_hi, m_lo, n_hi, n_lo, b_l)]
 
-    lib = _lib.load()
     e1 = facs[0]
     e2 = facs[1] if len(facs) == 2 else None
     out = torch.empty((), dtype=dt, device=dev)
-    es = A.t.element_size()
+    m_ext = ext[m_lo] if m_lo else 1
+    n_ext = ext[n_lo] if n_lo else 1
 
     def launch(kk, nbat, sa, sb, a_off, b_off, beta_, C_):
-        wsb = lib.tt_gemm_dot_workspace_bytes(code, M, N, nbat)
-        ws = _workspace(wsb, dev)
-        st = lib.tt_gemm_dot(
-            code, int(not la_[0]), int(lb_[0]), M, N, kk,
-            ctypes.c_void_p(A.t.data_ptr() + a_off * es), la_[1], sa,
-            ctypes.c_void_p(B.t.data_ptr() + b_off * es), lb_[1], sb, nbat,
-            ext[m_lo] if m_lo else 1, ext[n_lo] if n_lo else 1,
-            _ptr(e1.t), strides(e1), None if e2 is None else _ptr(e2.t), None if e2 is None else strides(e2),
-            float(alpha), float(beta_), _ptr(C_), _ptr(out), _ptr(ws), wsb, _stream_ptr(dev),
-        )
-        _lib.check(st, "tt_gemm_dot")
+        gemm_dot(not la_[0], lb_[0], M, N, kk, A.t, la_[1], sa, B.t, lb_[1], sb, nbat, m_ext, n_ext,
+                 e1.t, strides(e1), None if e2 is None else e2.t, None if e2 is None else strides(e2),
+                 alpha, beta_, C_, out, a_off, b_off)
 
     split = split_k(M, N, K, nb)
     if split <= 1:
