@@ -368,20 +368,23 @@ def bench_c1(torch, tt, dev, args):
                 e += (T * (2 * T - T.T) / d).sum().item()
         return e
 
-    loop()
-    t0 = time.perf_counter()
-    loop()
-    t_loop = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    for _ in range(20):
-        float(tt.mp2_energy(B, eo, ev))
-    t_fused = (time.perf_counter() - t0) / 20
+    def per_call(fn, reps, warm_s=0.3):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < warm_s:
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    t_loop = per_call(loop, 10)
+    t_fused = per_call(lambda: float(tt.mp2_energy(B, eo, ev)), 50)
     res = {"einsum_loop_ms": round(t_loop * 1e3, 3), "fused_cpu_operands_ms": round(t_fused * 1e3, 3)}
     if not args.no_cpu:
         from oracle import cpu_ref
 
         threads = cpu_threads(torch)
-        sec = cpu_timed(torch, lambda: cpu_ref.df_mp2_einsum_loop(B, eo, ev), reps=5)
+        sec = per_call(lambda: cpu_ref.df_mp2_einsum_loop(B, eo, ev), 10)
         res["cpu"] = {"einsum_loop_ms": round(sec * 1e3, 3), "cores": threads, "kind": "port",
                       "sample": "the reference example loop (64 einsum calls) on the same CPU tensors"}
     return res

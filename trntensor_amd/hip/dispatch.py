@@ -141,7 +141,12 @@ def place(*tensors: torch.Tensor) -> tuple[list[torch.Tensor], torch.device]:
     dev = cuda[0] if cuda else _device()
     if any(d != dev for d in cuda):
         raise RuntimeError(f"operands on different devices: {sorted({str(d) for d in cuda})}")
-    return [t if t.device == dev else t.to(dev) for t in tensors], orig
+    # When the result goes back to the host, the caller's blocking copy of the
+    # result orders after these uploads on the same stream, so they need not
+    # block on their own (pageable sources are staged by the runtime before
+    # the call returns). A device-resident result keeps blocking uploads.
+    nb = orig.type == "cpu"
+    return [t if t.device == dev else t.to(dev, non_blocking=nb) for t in tensors], orig
 
 
 _WIDEN = {torch.bfloat16: torch.float32, torch.float16: torch.float32}
