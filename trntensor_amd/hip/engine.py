@@ -340,6 +340,13 @@ def split_k(M: int, N: int, K: int, batch: int) -> int:
     return max(1, min(-(-512 // tiles), K // 512))
 
 
+def _slice_depth(K: int, split: int) -> int:
+    """K per slice: ceil(K / split) rounded up to the kernels' 16-deep stage,
+    so slice offsets keep 16-byte alignment and slices end on full stages."""
+    kc = -(-K // split)
+    return -(-kc // 16) * 16
+
+
 def _k_step(k_contiguous: bool, ld: int) -> int:
     """Element distance between consecutive k of an operand viewed rows x K."""
     return 1 if k_contiguous else ld
@@ -416,7 +423,7 @@ class _GemmRecipe:
                  self.ldd, self.sD, self.batch, alpha, beta, C, self.ldd, self.sD)
             return D
         M, N, K = self.M, self.N, self.K
-        kc = -(-K // self.split)
+        kc = _slice_depth(K, self.split)
         full, rem = K // kc, K % kc
         ka = _k_step(not self.ta, self.lda)  # X[m*lda + k] unless transposed
         kb = _k_step(self.tb, self.ldb)  # Y[n*ldb + k] when transposed
@@ -787,7 +794,7 @@ def contract_gemm_dot(
     # The dot is linear in the product, so K-slices (batch entries whose E
     # batch stride is 0) each contribute partials to the same sum; a last
     # shorter slice adds its share onto the first launch's result.
-    kc = -(-K // split)
+    kc = _slice_depth(K, split)
     full, rem = K // kc, K % kc
     ka = _k_step(la_[0], la_[1])
     kb = _k_step(lb_[0], lb_[1])
