@@ -308,7 +308,12 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // Small-M (e.g. the AO->MO half transform, M = nocc): 64 x 128 tiles of
     // four 32 x 64 wavefront tiles keep registers and LDS low enough for
     // several workgroups per CU, i.e. more loads in flight on a long stream.
-    if (g.M <= 64) return launch_tile<T, 64, 128, 2, 4, DOT>(g, ta, tb, vec, st);
+    // Batched short-K fp64 (e.g. 64 x 512^3): three 64 x 128 workgroups per
+    // CU instead of two 128 x 128 ones overlap one workgroup's prologue and
+    // epilogue with the others' MFMAs (measured 62% -> 70% of fp64 peak;
+    // unbatched and fp32 cases measured no gain).
+    if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
+        return launch_tile<T, 64, 128, 2, 4, DOT>(g, ta, tb, vec, st);
     if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4, DOT>(g, ta, tb, vec, st);
     return launch_tile<T, 128, 128, 4, 4, DOT>(g, ta, tb, vec, st);
 }
