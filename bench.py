@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5)")
+    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5,f1)")
     ap.add_argument("--skip-headline", action="store_true", help="run only the extra configs")
     ap.add_argument(
         "--calibrate-copy",
@@ -176,7 +176,7 @@ def main():
         return
     if args.skip_headline:
         extra = {}
-        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5"}
+        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1"}
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
         if "c4f32" in want:
@@ -187,6 +187,8 @@ def main():
             extra["c1_einsum_loop_fp32"] = bench_c1(torch, tt, dev, args)
         if "c5" in want:
             extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
+        if "f1" in want:
+            extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
         print(json.dumps({"configs": extra}))
         return
 
@@ -230,7 +232,7 @@ def main():
     del B, eo, ev
 
     extra = {}
-    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5"}
+    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1"}
     if not args.no_extra:
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
@@ -243,6 +245,8 @@ def main():
             extra["c1_einsum_loop_fp32"] = bench_c1(torch, tt, dev, args)
         if "c5" in want:
             extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
+        if "f1" in want:
+            extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
         line["configs"] = extra
 
     if not args.no_cpu:
@@ -285,6 +289,32 @@ def bench_c3(torch, tt, dev, args):
         "frac_binding_roofline": round(t_floor / t, 4),
         "bound": "mfma (AI 14.2 flop/B > fp64 ridge 9.8)",
         "kernel": "gemm_kernel<double,64,128,2,4,TA,!TB>",
+    }
+
+
+def bench_f1(torch, tt, dev, args):
+    """Full AO->MO transform at config-3 sizes with nvir = 320 (B[64, 320, 1536]),
+    then the fused MP2 energy on the device-resident B: the DF-MP2 pipeline
+    with nothing leaving HBM."""
+    print("bench: f1 ao->mo full + mp2", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    C = torch.linalg.qr(torch.randn(512, 384, generator=g, dtype=torch.float64))[0]
+    C_occ, C_vir = C[:, :64].contiguous().to(dev), C[:, 64:].contiguous().to(dev)
+    eri = torch.randn(512, 512, 1536, generator=g, dtype=torch.float64).to(dev)
+    eri = ((eri + eri.permute(1, 0, 2)) * (0.05 / 2**0.5)).contiguous()
+    eo = torch.sort(-20 + 19.7 * torch.rand(64, generator=g, dtype=torch.float64))[0].to(dev)
+    ev = torch.sort(0.1 + 4.9 * torch.rand(320, generator=g, dtype=torch.float64))[0].to(dev)
+    flop_t = 2 * 64 * 512 * 512 * 1536 + 2 * 64 * 320 * 1536 * 512
+    flop_e = 2080 * 2 * 320**2 * 1536
+    _, ms_t = timed_steady(torch, lambda: tt.ao_to_mo_transform(eri, C_occ, C_vir), max(5, args.steps))
+    _, ms_p = timed_steady(torch, lambda: tt.mp2_energy(tt.ao_to_mo_transform(eri, C_occ, C_vir), eo, ev), 5)
+    return {
+        "ao_to_mo_ms": round(ms_t, 4),
+        "ao_to_mo_TFLOP/s": round(flop_t / (ms_t * 1e-3) / 1e12, 2),
+        "ao_to_mo_frac_mfma": round(flop_t / (ms_t * 1e-3) / PEAK["f64"], 4),
+        "pipeline_ms": round(ms_p, 3),
+        "pipeline_TFLOP/s": round((flop_t + flop_e) / (ms_p * 1e-3) / 1e12, 2),
+        "shape": "eri[512,512,1536], C_occ[512,64], C_vir[512,320] -> B[64,320,1536] -> E",
     }
 
 
