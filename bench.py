@@ -20,6 +20,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -68,16 +69,68 @@ def timed(torch, fn, steps, warmup):
 
 
 def timed_steady(torch, fn, steps, min_warm_s=0.3):
-    """timed() after warming up for at least `min_warm_s` seconds of work (the
-    secondary configs follow host-side input generation, during which the GPU
-    idles and its clocks drop)."""
+    """(wall ms/step, median event ms/step) after warming up for at least
+    `min_warm_s` seconds of work (the secondary configs follow host-side input
+    generation, during which the GPU idles and its clocks drop)."""
     t0 = time.perf_counter()
     n = 0
     while n < 2 or time.perf_counter() - t0 < min_warm_s:
         fn()
         torch.cuda.synchronize()
         n += 1
-    return timed(torch, fn, steps, 0)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def measured_peaks(torch, dev):
+    """Rates this device sustains in microbenchmarks: fp64/fp32 MFMA with no
+    memory traffic (tt_mfma_rate_probe) and a 1 GiB device-to-device copy
+    (bytes read + written). The datasheet peaks assume the maximum clock;
+    these are what the kernels' fractions can also be read against."""
+    from trntensor_amd.hip import _lib
+
+    lib = _lib.load()
+    st = torch.cuda.current_stream(dev).cuda_stream
+    wgs = 1024
+    out = {}
+    for key, code, dt in (("mfma_f64_TFLOPs", _lib.TT_F64, torch.float64), ("mfma_f32_TFLOPs", _lib.TT_F32, torch.float32)):
+        buf = torch.empty(wgs, dtype=dt, device=dev)
+        iters = 20000 if code == _lib.TT_F64 else 40000
+        flop = wgs * 4 * iters * 8 * 2048
+
+        def run():
+            _lib.check(lib.tt_mfma_rate_probe(code, wgs, iters, buf.data_ptr(), st), "tt_mfma_rate_probe")
+
+        _, ms = timed_steady(torch, run, 10)
+        out[key] = round(flop / (ms * 1e-3) / 1e12, 2)
+    x = torch.ones(1 << 27, dtype=torch.float64, device=dev)
+    y = torch.empty_like(x)
+    _, ms = timed_steady(torch, lambda: y.copy_(x), 10)
+    out["hbm_copy_GBps"] = round(2 * x.numel() * 8 / (ms * 1e-3) / 1e9, 1)
+    del x, y
+    return out
+
+
+def host_info(torch):
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    found = re.search(r"BLAS_INFO=([^,\s]+)", torch.__config__.show())
+    blas = found.group(1) if found else "unknown"
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "torch": torch.__version__, "blas": blas}
 
 
 def mp2_inputs(torch, dtype, nocc=64, nvir=320, naux=1200):
@@ -230,6 +283,10 @@ def main():
         },
     }
     del B, eo, ev
+    print("bench: measured peaks (MFMA probe, device copy)", file=sys.stderr, flush=True)
+    peaks = measured_peaks(torch, dev)
+    line["measured_peaks"] = peaks
+    line["roofline"]["frac_measured_peak"] = round(achieved / 1e12 / peaks["mfma_f64_TFLOPs"], 4)
 
     extra = {}
     want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1"}
@@ -252,6 +309,7 @@ def main():
     if not args.no_cpu:
         print("bench: cpu baseline (reference loop sample)", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_mp2_baseline(torch)
+        line["cpu_baseline"]["host"] = host_info(torch)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

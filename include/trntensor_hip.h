@@ -181,6 +181,17 @@ int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape,
                         const void* C, void* D, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/*
+ * Measurement aid with no counterpart in the reference: `workgroups`
+ * workgroups of 4 wavefronts each run `iters` rounds of 8 independent
+ * 16x16x4 MFMA accumulator chains of `dtype` (TT_F32 or TT_F64) from register
+ * operands, 8 * 2048 FLOP per wavefront per round, and write one value per
+ * workgroup to out (device, `workgroups` elements of dtype). Timing it gives
+ * the MFMA rate the device sustains without memory traffic, the measured
+ * peak that the benchmark reports next to the datasheet peak.
+ */
+int tt_mfma_rate_probe(int dtype, int64_t workgroups, int64_t iters, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
