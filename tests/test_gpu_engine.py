@@ -97,3 +97,47 @@ def test_fused_dot_mappings(hip, gterms, xname, shapes, factors):
     want = 1.5 * float((X * E).sum()) + 0.5 * 0.75
     scale = 1.5 * float((X.abs() * E.abs()).sum()) + 0.5 * 0.75
     assert abs(float(got) - want) <= 1e-13 * scale
+
+
+class TestIndexRange:
+    """Outputs and reductions beyond 2^31 elements: the strided kernel takes
+    32-bit linear indices, so the engine splits such launches; the GEMM core
+    addresses with 64-bit offsets. Checked on sampled entries."""
+
+    def test_outer_product_beyond_2_31(self, hip):
+        n = 48000  # 2.30e9 outputs, 9.2 GB in float32
+        a = torch.arange(n, dtype=torch.float32, device="cuda") % 1021 - 510
+        b = torch.arange(n, dtype=torch.float32, device="cuda") % 997 - 498
+        out = engine.contract(["i", "j"], "ij", [a, b])
+        assert out.shape == (n, n)
+        idx = torch.randint(0, n, (4096, 2), generator=torch.Generator().manual_seed(0))
+        got = out[idx[:, 0], idx[:, 1]].cpu()
+        want = (idx[:, 0] % 1021 - 510).float() * (idx[:, 1] % 997 - 498).float()
+        assert torch.equal(got, want)
+        # the last row and column (the split's final chunk)
+        assert float(out[n - 1, n - 1]) == float(((n - 1) % 1021 - 510) * ((n - 1) % 997 - 498))
+        del out
+
+    def test_sum_beyond_2_31(self, hip):
+        n = (1 << 31) + 4097  # reduction length past 2^31, 8.6 GB of float32 ones
+        x = torch.ones(n, dtype=torch.float32, device="cuda")
+        # The launch is split at 2^31 and the second part accumulates onto
+        # the first. Every per-thread and per-block partial is an integer
+        # below 2^24 (exact in float32); only the final sum rounds (2^31 + 4097
+        # is not a float32), hence the relative bar.
+        got = float(engine.contract(["i"], "", [x]))
+        assert abs(got - n) / n < 1e-6
+        del x
+
+    def test_gemm_output_beyond_2_31(self, hip):
+        M, N = 50000, 45000  # 2.25e9 outputs, K = 2
+        A = (torch.arange(M * 2, dtype=torch.float32, device="cuda") % 7 - 3).view(M, 2)
+        B = (torch.arange(2 * N, dtype=torch.float32, device="cuda") % 5 - 2).view(2, N)
+        D = engine.contract(["ik", "kj"], "ij", [A, B], prefer_gemm=True)
+        idx_m = torch.randint(0, M, (2048,), generator=torch.Generator().manual_seed(1))
+        idx_n = torch.randint(0, N, (2048,), generator=torch.Generator().manual_seed(2))
+        got = D[idx_m, idx_n].cpu()
+        want = (A.cpu()[idx_m] * B.cpu()[:, idx_n].T).sum(1)
+        assert torch.equal(got, want)
+        assert float(D[M - 1, N - 1]) == float((A[M - 1] * B[:, N - 1]).sum())
+        del D
