@@ -138,3 +138,26 @@ def test_mp2_config4_invariants(hip, config4):
     perm = torch.randperm(B.shape[1], generator=torch.Generator().manual_seed(1)).cuda()
     assert rel(tt.mp2_energy(B[:, perm].contiguous(), eo, ev[perm]), e0) <= 1e-11
     assert e0 < 0.0
+
+
+def test_mp2_operand_beyond_2_31_elements(hip):
+    """B with more than 2^31 elements (17 GB): the panel offsets are 64-bit.
+    B[i, a, P] = x_i y_a z_P gives T_ijab = x_i x_j y_a y_b S with
+    S = sum_P z_P^2 (exact here), so E = S^2 E_1 where E_1 is the naux = 1
+    closed form (oracle/brute.mp2_energy_rank1)."""
+    nocc, nvir = 3, 70  # ragged virtual block (64 + 6)
+    naux = (1 << 31) // (nocc * nvir) + 4099
+    assert nocc * nvir * naux > (1 << 31)
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(nocc, generator=g, dtype=torch.float64) * 0.2 + 0.1
+    y = torch.rand(nvir, generator=g, dtype=torch.float64) * 0.2 - 0.1
+    eo = torch.sort(-20 + 19.7 * torch.rand(nocc, generator=g, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(nvir, generator=g, dtype=torch.float64))[0]
+    pattern = torch.tensor([1.0, -0.5, 0.5, -1.0], dtype=torch.float64, device="cuda")
+    z = pattern.repeat((naux + 3) // 4)[:naux]
+    S = float((z * z).sum())  # sums of 1 and 0.25: exact
+    B = x.cuda()[:, None, None] * y.cuda()[None, :, None] * z[None, None, :]
+    e = float(tt.mp2_energy(B, eo.cuda(), ev.cuda()))
+    del B
+    want = S * S * brute.mp2_energy_rank1(x.numpy(), y.numpy(), eo.numpy(), ev.numpy())
+    assert rel(e, want) <= 1e-10, (e, want)
