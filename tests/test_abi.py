@@ -88,8 +88,13 @@ def test_strided_workspace_only_for_split_reductions(lib):
     one = _lib.i64_array([1])
     red = _lib.i64_array([10_000_000])
     assert lib.tt_strided_contract_workspace_bytes(1, 1, one, 1, red) > 0
-    many = _lib.i64_array([100_000])
+    # column tiles may split the reduction of up to 2^18 outputs
+    some = _lib.i64_array([100_000])
+    assert lib.tt_strided_contract_workspace_bytes(1, 1, some, 1, red) > 0
+    many = _lib.i64_array([1 << 18])
     assert lib.tt_strided_contract_workspace_bytes(1, 1, many, 1, red) == 0
+    short = _lib.i64_array([1])
+    assert lib.tt_strided_contract_workspace_bytes(1, 1, many, 1, short) == 0
 
 
 # ---------------------------------------------------------------------------

@@ -118,3 +118,51 @@ def test_strided_split_reduction_matches_single_pass(hip):
     res = engine.contract(["ij", "ij"], "i", [x.cuda(), y.cuda()])
     ref = (x * y).sum(1)
     assert normwise(res, ref) <= 1e-12
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize(
+    "sub,shapes",
+    [
+        # column tiles: the output's innermost letter is the operands' contiguous one
+        ("ijk->k", [(70, 300, 129)]),
+        ("ijk->jk", [(500, 33, 260)]),
+        ("ijk,ijk->k", [(40, 300, 77), (40, 300, 77)]),
+        ("ij,ij->j", [(5000, 3)]),
+        # transpose tiles: permutations whose innermost output letter is strided
+        ("ij->ji", [(1000, 333)]),
+        ("ijk->kji", [(70, 65, 130)]),
+        ("abcd->dbca", [(9, 70, 5, 66)]),
+        ("abc->bca", [(130, 3, 200)]),
+    ],
+)
+def test_strided_schedules(hip, dt, sub, shapes):
+    """The column-tile and transpose-tile schedules against float64 numpy,
+    with and without the alpha/beta epilogue."""
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(7)
+    lhs, out = sub.split("->")
+    terms = lhs.split(",")
+    if len(terms) == 2 and len(shapes) == 1:
+        shapes = shapes * 2
+    ops = [torch.randn(*s, generator=g, dtype=torch.float64) for s in shapes]
+    ref = torch.from_numpy(np.asarray(brute.einsum_f64(sub, *[o.numpy() for o in ops])))
+    res = engine.contract(terms, out, [o.to("cuda", dt) for o in ops])
+    assert normwise(res, ref) <= (1e-12 if dt == torch.float64 else 1e-5)
+    C = torch.randn(*ref.shape, generator=g, dtype=torch.float64)
+    res = engine.contract(terms, out, [o.to("cuda", dt) for o in ops], 1.5, -0.5, C.to("cuda", dt))
+    assert normwise(res, 1.5 * ref - 0.5 * C) <= (1e-12 if dt == torch.float64 else 1e-5)
+
+
+def test_coltile_double_double(hip):
+    """'ijk->k' through the column-tile schedule with double-double partials:
+    sums that cancel to a few units are exact, where float64 partials are not."""
+    from trntensor_amd.hip import engine
+
+    n = 1 << 16
+    base = torch.tensor([1e16, 1.0, -1e16, 1.0], dtype=torch.float64)
+    x = base.repeat(n // 4)[:, None].expand(n, 96).contiguous().view(n // 64, 64, 96)
+    with engine.accumulation("dd"):
+        got = engine.contract(["ijk"], "k", [x.cuda()])
+    assert torch.equal(got.cpu(), torch.full((96,), float(n // 2), dtype=torch.float64))

@@ -1,13 +1,21 @@
 // Strided multiply-reduce for contractions without a GEMM shape:
 //   D[o] = alpha * sum_r A[a_off(o) + a_roff(r)] * B[b_off(o) + b_roff(r)] (+ beta * C[o])
 //
-// Two schedules, chosen on the host:
-//  - one thread per output element (many outputs: outer products,
-//    permutations, small per-output reductions), grid-stride over outputs;
-//  - one workgroup per (output, reduction slice) (few outputs, long
-//    reductions: dots, traces, full contractions): 256 threads stride the
-//    slice, reduce with wavefront shuffles, and either finish the output or
-//    write a partial that a second kernel sums in a fixed order.
+// Four schedules, chosen on the host from extents and strides:
+//  - per output: one thread per output element, grid-stride (many outputs:
+//    outer products, elementwise products, short per-output reductions);
+//  - per block: one workgroup per (output, reduction slice) (few outputs,
+//    long reductions over the operands' contiguous dimension: dots, traces):
+//    256 threads stride the slice, reduce with wavefront shuffles, and either
+//    finish the output or write a partial that a second kernel sums in a
+//    fixed order;
+//  - column tiles: 256 consecutive outputs per workgroup times reduction
+//    slices, when the output's innermost dimension is the operands'
+//    contiguous one ('ijk->k'): each thread reduces one output over a slice,
+//    so every load instruction reads consecutive addresses; partials as above;
+//  - transpose tiles: a single-operand permutation whose output innermost
+//    dimension is not the operand's contiguous one ('ijk->kji'): 64 x 64
+//    tiles pass through LDS so both the reads and the writes are coalesced.
 // Multi-indices are decoded with precomputed fast-division multipliers; the
 // host splits any launch whose index range would reach 2^31.
 #include "tt_common.hpp"
@@ -179,24 +187,119 @@ __global__ __launch_bounds__(256) void strided_finish_kernel(StridedArgs g) {
     }
 }
 
-// Host-side schedule choice shared by the workspace query and the launch.
+// Grid: (ceil(n_out / 256), nsplit). Thread t of workgroup (x, s) reduces
+// output 256 x + t over the s-th contiguous slice of the reduction range.
+template <typename T, bool DD>
+__global__ __launch_bounds__(256) void strided_coltile_kernel(StridedArgs g) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= g.n_out) return;
+    const T* A = static_cast<const T*>(g.A);
+    const T* B = static_cast<const T*>(g.B);
+    int64_t oa, ob;
+    decode((uint32_t)o, g.out, oa, ob);
+    const int64_t chunk = (g.n_red + g.nsplit - 1) / g.nsplit;
+    const int64_t r0 = (int64_t)blockIdx.y * chunk;
+    const int64_t r1 = min(g.n_red, r0 + chunk);
+    Acc<T, DD> acc;
+    for (int64_t r = r0; r < r1; ++r) {
+        int64_t ra, rb;
+        decode((uint32_t)r, g.red, ra, rb);
+        const T x = A[oa + ra];
+        if (B) acc.add_prod(x, B[ob + rb]);
+        else acc.add(x);
+    }
+    if (g.nsplit == 1) static_cast<T*>(g.D)[o] = finish<T, DD>(g, o, acc);
+    else acc.store_partial(g.partial, (int64_t)blockIdx.y * g.n_out + o, g.nsplit * g.n_out);
+}
+
+// Permutation through LDS. Output dimension u is the output's innermost
+// (D stride 1), v the dimension along which A is contiguous; the remaining
+// output dimensions form `bat` (A and D strides). Workgroup: one 64 (u) x 64
+// (v) tile of one batch index; threads read along v and write along u.
+struct TransArgs {
+    int64_t U, V;      // extents of u and v
+    int64_t sa_u, sa_v, sd_v;
+    int64_t tiles_u, tiles_v;
+    Dims bat;          // sa = A strides, sb = D strides
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void strided_transpose_kernel(StridedArgs g, TransArgs t) {
+    __shared__ T tile[64][65];
+    const int64_t per = t.tiles_u * t.tiles_v;
+    const int64_t z = blockIdx.x / per;
+    const int64_t rem = blockIdx.x - z * per;
+    const int64_t u0 = (rem % t.tiles_u) * 64;
+    const int64_t v0 = (rem / t.tiles_u) * 64;
+    int64_t za, zd;
+    decode((uint32_t)z, t.bat, za, zd);
+    const T* A = static_cast<const T*>(g.A);
+    const int lo = threadIdx.x & 63;
+    const int hi = threadIdx.x >> 6;
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+        const int ul = hi + 4 * i;
+        const int64_t u = u0 + ul, v = v0 + lo;
+        if (u < t.U && v < t.V) tile[ul][lo] = A[za + u * t.sa_u + v * t.sa_v];
+    }
+    __syncthreads();
+    T* D = static_cast<T*>(g.D);
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+        const int vl = hi + 4 * i;
+        const int64_t u = u0 + lo, v = v0 + vl;
+        if (u < t.U && v < t.V) {
+            const int64_t o = zd + v * t.sd_v + u;
+            T x = tile[lo][vl];
+            if (g.alpha != 1.0) x = (T)g.alpha * x;
+            if (g.C) x = x + (T)g.beta * static_cast<const T*>(g.C)[o];
+            D[o] = x;
+        }
+    }
+}
+
+// Host-side schedule choice. The workspace query sees only extents, so it
+// reserves the larger partial buffer of the two split schedules the extents
+// allow; the launch then picks with the strides.
+enum Kind { PER_OUTPUT, PER_BLOCK, COLTILE, TRANSPOSE };
+
 struct Plan {
-    bool per_block;
+    Kind kind;
     int64_t nsplit;
 };
 
-static Plan choose(int64_t n_out, int64_t n_red) {
-    Plan p{false, 1};
-    if (n_red > 1 && n_out < 8192) {
-        p.per_block = true;
-        // Enough workgroups to fill 256 CUs several times, each at least 2K elements.
-        int64_t want = (4096 + n_out - 1) / n_out;
-        int64_t cap = (n_red + 2047) / 2048;
-        p.nsplit = want < cap ? want : cap;
-        if (p.nsplit < 1) p.nsplit = 1;
-        if (p.nsplit > 65535) p.nsplit = 65535;
+static int64_t per_block_split(int64_t n_out, int64_t n_red) {
+    // Enough workgroups to fill 256 CUs several times, each at least 2K elements.
+    int64_t want = (4096 + n_out - 1) / n_out;
+    int64_t cap = (n_red + 2047) / 2048;
+    int64_t n = want < cap ? want : cap;
+    return n < 1 ? 1 : (n > 65535 ? 65535 : n);
+}
+
+static int64_t coltile_split(int64_t n_out, int64_t n_red) {
+    // ~2048 workgroups in all, each thread at least 64 reduction elements.
+    const int64_t bx = (n_out + 255) / 256;
+    int64_t want = (2048 + bx - 1) / bx;
+    int64_t cap = (n_red + 63) / 64;
+    int64_t n = want < cap ? want : cap;
+    return n < 1 ? 1 : (n > 65535 ? 65535 : n);
+}
+
+constexpr int64_t kColtileMaxOut = 1 << 18;
+
+static bool per_block_fits(int64_t n_out, int64_t n_red) { return n_red > 1 && n_out < 8192; }
+static bool coltile_fits(int64_t n_out, int64_t n_red) { return n_red > 1 && n_out < kColtileMaxOut; }
+
+static Plan choose(const StridedArgs& g) {
+    const int last = g.out.n - 1;
+    const bool out_contig = last >= 0 && g.out.sa[last] == 1 && (!g.B || g.out.sb[last] == 0 || g.out.sb[last] == 1);
+    if (g.red.n == 0 && !g.B && g.out.n >= 2 && g.n_out >= 4096 && g.out.sa[last] != 1) {
+        for (int k = 0; k < last; ++k)
+            if (g.out.sa[k] == 1) return Plan{TRANSPOSE, 1};
     }
-    return p;
+    if (out_contig && coltile_fits(g.n_out, g.n_red)) return Plan{COLTILE, coltile_split(g.n_out, g.n_red)};
+    if (per_block_fits(g.n_out, g.n_red)) return Plan{PER_BLOCK, per_block_split(g.n_out, g.n_red)};
+    return Plan{PER_OUTPUT, 1};
 }
 
 static int64_t prod(int n, const int64_t* s) {
@@ -205,20 +308,64 @@ static int64_t prod(int n, const int64_t* s) {
     return r;
 }
 
+template <typename T>
+static int launch_transpose(StridedArgs& g, const int64_t* out_shape, hipStream_t st) {
+    const int last = g.out.n - 1;
+    int v = -1;
+    for (int k = 0; k < last; ++k)
+        if (g.out.sa[k] == 1) {
+            v = k;
+            break;
+        }
+    int64_t dstride[TT_MAX_DIMS];
+    int64_t acc = 1;
+    for (int k = last; k >= 0; --k) {
+        dstride[k] = acc;
+        acc *= out_shape[k];
+    }
+    TransArgs t;
+    t.U = out_shape[last];
+    t.V = out_shape[v];
+    t.sa_u = g.out.sa[last];
+    t.sa_v = g.out.sa[v];
+    t.sd_v = dstride[v];
+    t.tiles_u = (t.U + 63) / 64;
+    t.tiles_v = (t.V + 63) / 64;
+    t.bat.n = 0;
+    int64_t nbat = 1;
+    for (int k = 0; k < last; ++k) {
+        if (k == v) continue;
+        const int b = t.bat.n++;
+        t.bat.div[b] = make_fastdiv((uint32_t)out_shape[k]);
+        t.bat.sa[b] = g.out.sa[k];
+        t.bat.sb[b] = dstride[k];
+        nbat *= out_shape[k];
+    }
+    const int64_t blocks = t.tiles_u * t.tiles_v * nbat;
+    if (blocks > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_strided_contract: %lld tiles", (long long)blocks);
+    hipLaunchKernelGGL((strided_transpose_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st, g, t);
+    return TT_OK;
+}
+
 template <typename T, bool DD>
-static int run_typed(StridedArgs g, int n_out_dims, const int64_t* out_shape, hipStream_t st) {
-    const Plan pl = choose(g.n_out, g.n_red);
+static int run_typed(StridedArgs g, const int64_t* out_shape, hipStream_t st) {
+    const Plan pl = choose(g);
     g.nsplit = pl.nsplit;
-    if (!pl.per_block) {
+    if (pl.kind == TRANSPOSE) {
+        const int rc = launch_transpose<T>(g, out_shape, st);
+        if (rc != TT_OK) return rc;
+    } else if (pl.kind == PER_OUTPUT) {
         int64_t blocks = (g.n_out + 255) / 256;
         if (blocks > 1 << 20) blocks = 1 << 20;
         if (blocks > 0) hipLaunchKernelGGL((strided_per_output_kernel<T, DD>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+    } else if (pl.kind == COLTILE) {
+        const unsigned bx = (unsigned)((g.n_out + 255) / 256);
+        hipLaunchKernelGGL((strided_coltile_kernel<T, DD>), dim3(bx, (unsigned)g.nsplit), dim3(256), 0, st, g);
+        if (g.nsplit > 1) hipLaunchKernelGGL((strided_finish_kernel<T, DD>), dim3((unsigned)g.n_out), dim3(256), 0, st, g);
     } else {
         hipLaunchKernelGGL((strided_per_block_kernel<T, DD>), dim3((unsigned)g.n_out, (unsigned)g.nsplit), dim3(256), 0, st, g);
         if (g.nsplit > 1) hipLaunchKernelGGL((strided_finish_kernel<T, DD>), dim3((unsigned)g.n_out), dim3(256), 0, st, g);
     }
-    (void)n_out_dims;
-    (void)out_shape;
     return check_launch("tt_strided_contract");
 }
 
@@ -229,11 +376,16 @@ extern "C" size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, cons
     using namespace tt;
     if (n_out < 0 || n_red < 0 || n_out > TT_MAX_DIMS || n_red > TT_MAX_DIMS) return 0;
     const int64_t no = prod(n_out, out_shape), nr = prod(n_red, red_shape);
-    const Plan p = choose(no, nr);
-    if (!p.per_block || p.nsplit == 1) return 0;
+    int64_t parts = 0;
+    if (per_block_fits(no, nr)) parts = per_block_split(no, nr);
+    if (coltile_fits(no, nr)) {
+        const int64_t c = coltile_split(no, nr);
+        parts = c > parts ? c : parts;
+    }
+    if (parts <= 1) return 0;
     // TT_F64_DD partials are (p, s) pairs of doubles.
     const size_t es = dtype == TT_F64_DD ? 16 : dtype == TT_F64 ? 8 : 4;
-    return ((size_t)(p.nsplit * no) * es + 255) / 256 * 256;
+    return ((size_t)(parts * no) * es + 255) / 256 * 256;
 }
 
 extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape, const int64_t* a_out_strides,
@@ -287,7 +439,7 @@ extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shap
         // Empty reduction: every output is alpha * 0 (+ beta * C).
         g.n_red = 0;
     }
-    if (dtype == TT_F64_DD) return run_typed<double, true>(g, n_out, out_shape, st);
-    if (dtype == TT_F64) return run_typed<double, false>(g, n_out, out_shape, st);
-    return run_typed<float, false>(g, n_out, out_shape, st);
+    if (dtype == TT_F64_DD) return run_typed<double, true>(g, out_shape, st);
+    if (dtype == TT_F64) return run_typed<double, false>(g, out_shape, st);
+    return run_typed<float, false>(g, out_shape, st);
 }
