@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5,f1)")
+    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5,f1,a5)")
     ap.add_argument("--skip-headline", action="store_true", help="run only the extra configs")
     ap.add_argument(
         "--calibrate-copy",
@@ -229,7 +229,7 @@ def main():
         return
     if args.skip_headline:
         extra = {}
-        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1"}
+        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1", "a5"}
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
         if "c4f32" in want:
@@ -242,6 +242,8 @@ def main():
             extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
         if "f1" in want:
             extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
+        if "a5" in want:
+            extra["a5_strided_patterns"] = bench_a5(torch, tt, dev, args)
         print(json.dumps({"configs": extra}))
         return
 
@@ -289,7 +291,7 @@ def main():
     line["roofline"]["frac_measured_peak"] = round(achieved / 1e12 / peaks["mfma_f64_TFLOPs"], 4)
 
     extra = {}
-    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1"}
+    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1", "a5"}
     if not args.no_extra:
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
@@ -304,6 +306,8 @@ def main():
             extra["c5_greedy_path_fp64"] = bench_c5(torch, tt, dev, args)
         if "f1" in want:
             extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
+        if "a5" in want:
+            extra["a5_strided_patterns"] = bench_a5(torch, tt, dev, args)
         line["configs"] = extra
 
     if not args.no_cpu:
@@ -348,6 +352,41 @@ def bench_c3(torch, tt, dev, args):
         "bound": "mfma (AI 14.2 flop/B > fp64 ridge 9.8)",
         "kernel": "gemm_kernel<double,64,128,2,4,TA,!TB>",
     }
+
+
+def bench_a5(torch, tt, dev, args):
+    """'torch'-strategy contractions without a GEMM shape (tt_strided_contract):
+    HBM-bound permutations and reductions on 1 GiB operands. Bytes = operand
+    read once + output written once; bound = HBM."""
+    print("bench: a5 strided patterns", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(512, 512, 512, generator=g, dtype=torch.float64)
+    T = torch.randn(16384, 16384, generator=g, dtype=torch.float32)
+    Xd, Td = X.to(dev), T.to(dev)
+    cases = [
+        ("ijk->kji", Xd, X, 2 * X.numel() * 8),
+        ("ijk->ikj", Xd, X, 2 * X.numel() * 8),
+        ("ijk->k", Xd, X, X.numel() * 8),
+        ("ijk->i", Xd, X, X.numel() * 8),
+        ("ij->ji", Td, T, 2 * T.numel() * 4),
+    ]
+    out = {}
+    for sub, d, h, byt in cases:
+        _, ms = timed_steady(torch, lambda: tt.einsum(sub, d), max(5, args.steps))
+        r = {"ms": round(ms, 4), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1),
+             "frac_hbm": round(byt / (ms * 1e-3) / PEAK["hbm"], 4)}
+        if not args.no_cpu:
+            from oracle import cpu_ref
+
+            threads = cpu_threads(torch)
+            # torch.einsum returns a permuted view for a pure permutation; the
+            # baseline materialises it (.contiguous()) like the GPU result.
+            sec = cpu_timed(torch, lambda: cpu_ref.einsum(sub, h).contiguous(), reps=1)
+            r["cpu"] = {"ms": round(sec * 1e3, 2), "GB/s": round(byt / sec / 1e9, 2), "cores": threads, "kind": "port",
+                        "sample": "full operand through the reference's 'torch' strategy (torch.einsum), "
+                                  "materialised with .contiguous()"}
+        out[f"{sub} {str(h.dtype).replace('torch.', '')}"] = r
+    return out
 
 
 def bench_f1(torch, tt, dev, args):
