@@ -17,7 +17,9 @@
  *  - dtype codes: TT_F32 = 0 (float), TT_F64 = 1 (double). TT_F64_DD = 2
  *    (tt_gemm, tt_strided_contract only): double data, every product formed
  *    exactly and summed in double-double (Ogita-Rump-Oishi Dot2), rounded
- *    to double once per output.
+ *    to double once per output. TT_BF16 = 3, TT_F16 = 4 (tt_gemm only):
+ *    16-bit A, B, C, D; products and sums in fp32 on the 16-bit MFMA, alpha
+ *    and beta applied in fp32, one rounding at the store.
  *  - Return codes: TT_OK 0; TT_INVALID 1 (bad argument: the Python layer
  *    raises ValueError); TT_UNSUPPORTED 2 (dtype/shape the kernels do not
  *    cover: NotImplementedError); TT_HIP_ERROR 3 (launch failure:
@@ -38,7 +40,7 @@ extern "C" {
 #define TT_MAX_DIMS 8
 
 enum { TT_OK = 0, TT_INVALID = 1, TT_UNSUPPORTED = 2, TT_HIP_ERROR = 3 };
-enum { TT_F32 = 0, TT_F64 = 1, TT_F64_DD = 2 };
+enum { TT_F32 = 0, TT_F64 = 1, TT_F64_DD = 2, TT_BF16 = 3, TT_F16 = 4 };
 
 /* ABI version of the loaded library (TT_ABI_VERSION at build time). */
 int tt_abi_version(void);

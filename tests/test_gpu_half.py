@@ -1,0 +1,89 @@
+"""bfloat16 / float16 contractions: GEMM shapes run on the 16-bit MFMA GEMM
+(tt_gemm with TT_BF16 / TT_F16: fp32 products and sums, alpha/beta in fp32,
+one rounding at the store); every other shape is widened to float32.
+
+The reference computes these in torch on the CPU in the 16-bit dtype
+(trntensor/einsum.py:94-103 with dtype="bf16"), whose rounding of partial
+results is torch's own. The expected value here is the float32 product of the
+same 16-bit inputs (exact widening), rounded once to the 16-bit dtype; the
+bar is normwise 1e-2 (bf16, 8-bit mantissa) and 2e-3 (fp16), i.e. a few
+16-bit ulps plus fp32 summation-order differences.
+"""
+
+import pytest
+import torch
+
+import trntensor_amd as trntensor
+from tests.util import normwise
+from trntensor_amd.hip import engine
+
+pytestmark = pytest.mark.gpu
+
+BAR = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
+
+
+def _native_used(dt):
+    return any(k[7] == dt for k in engine._RECIPES)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "sub,shapes",
+    [
+        ("ij,jk->ik", [(256, 192), (192, 384)]),
+        ("ij,jk->ik", [(200, 150), (150, 130)]),  # ragged tiles and K
+        ("ji,jk->ik", [(150, 200), (150, 130)]),
+        ("ij,kj->ik", [(200, 150), (130, 150)]),
+        ("ji,kj->ik", [(150, 200), (130, 150)]),
+        ("ij,jk->ki", [(200, 150), (150, 130)]),  # swapped output
+        ("bij,bjk->bik", [(3, 130, 70), (3, 70, 140)]),
+        ("ap,bp->ab", [(320, 1200), (320, 1200)]),  # DF-MP2 pair block
+    ],
+)
+def test_gemm_shapes_native(hip, dt, sub, shapes):
+    g = torch.Generator().manual_seed(5)
+    ops = [torch.randn(*s, generator=g).to(dt) for s in shapes]
+    engine._RECIPES.clear()
+    got = trntensor.einsum(sub, *[o.cuda() for o in ops])
+    assert got.dtype == dt
+    assert _native_used(dt)
+    want = torch.einsum(sub, *[o.float() for o in ops]).to(dt)
+    assert normwise(got.float(), want.float()) <= BAR[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_alpha_beta_out(hip, dt):
+    g = torch.Generator().manual_seed(6)
+    A, B, C = (torch.randn(*s, generator=g).to(dt) for s in ((130, 90), (90, 150), (130, 150)))
+    got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), alpha=1.5, beta=-0.5, out=C.cuda())
+    want = (1.5 * (A.float() @ B.float()) - 0.5 * C.float()).to(dt)
+    assert normwise(got.float(), want.float()) <= BAR[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    "sub,shapes",
+    [
+        ("ij,ij->", [(64, 80), (64, 80)]),  # no GEMM shape: widened
+        ("ijk,jk->i", [(40, 30, 20), (30, 20)]),  # K over two letters in place
+        ("iaj,jb->iab", [(20, 30, 40), (40, 50)]),
+    ],
+)
+def test_other_shapes(hip, dt, sub, shapes):
+    g = torch.Generator().manual_seed(7)
+    ops = [torch.randn(*s, generator=g).to(dt) for s in shapes]
+    got = trntensor.einsum(sub, *[o.cuda() for o in ops])
+    assert got.dtype == dt
+    want = torch.einsum(sub, *[o.float() for o in ops]).to(dt)
+    assert normwise(got.float(), want.float()) <= BAR[dt]
+
+
+def test_dtype_string_bf16_large(hip):
+    """einsum(dtype="bf16") on fp32 inputs at 2048^3: cast, native GEMM, bf16 result."""
+    g = torch.Generator().manual_seed(8)
+    A = torch.randn(2048, 2048, generator=g).cuda()
+    B = torch.randn(2048, 2048, generator=g).cuda()
+    got = trntensor.einsum("ij,jk->ik", A, B, dtype="bf16")
+    assert got.dtype == torch.bfloat16
+    want = (A.bfloat16().float() @ B.bfloat16().float()).bfloat16()
+    assert normwise(got.float(), want.float()) <= 1e-2

@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libtrntensor_hip.so")
-SOURCES = ["tt_abi.hip", "tt_dd.hip", "tt_gemm.hip", "tt_mp2.hip", "tt_probe.hip", "tt_strided.hip"]
+SOURCES = ["tt_abi.hip", "tt_dd.hip", "tt_gemm.hip", "tt_gemm16.hip", "tt_mp2.hip", "tt_probe.hip", "tt_strided.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -324,7 +324,8 @@ int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (dtype == TT_F64) return gemm_typed<double, false>(g, ta, tb, st);
     if (dtype == TT_F32) return gemm_typed<float, false>(g, ta, tb, st);
     if (dtype == TT_F64_DD) return gemm_dd_dispatch(ta, tb, g, st);
-    return set_error(TT_UNSUPPORTED, "tt_gemm: dtype %d (only TT_F32, TT_F64, TT_F64_DD)", dtype);
+    if (dtype == TT_BF16 || dtype == TT_F16) return gemm16_dispatch(dtype, ta, tb, g, st);
+    return set_error(TT_UNSUPPORTED, "tt_gemm: dtype %d (only TT_F32, TT_F64, TT_F64_DD, TT_BF16, TT_F16)", dtype);
 }
 
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts) {

@@ -32,6 +32,8 @@ struct GemmArgs {
 int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // Double-double GEMM (dtype TT_F64_DD) on the vector ALUs; same arguments.
 int gemm_dd_dispatch(bool ta, bool tb, GemmArgs& g, hipStream_t st);
+// 16-bit GEMM (dtype TT_BF16 / TT_F16) on the 16x16x32 MFMA; same arguments.
+int gemm16_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // Dot epilogue; writes one double per workgroup to g.partial and returns the
 // number of workgroups in *nparts.
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);

@@ -108,7 +108,14 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
     if len(dts) > 1:
         raise RuntimeError(f"einsum(): operands must share one dtype, got {sorted(str(d) for d in dts)}")
     res_dtype = ops[0].dtype
-    cd = cd_override or (torch.float64 if plan.precision == "kahan" else dispatch.compute_dtype(res_dtype))
+    if cd_override is not None:
+        cd = cd_override
+    elif plan.precision == "kahan":
+        cd = torch.float64
+    elif res_dtype in (torch.bfloat16, torch.float16) and len(ops) == 2 and plan.strategy != "path":
+        cd = res_dtype  # the engine runs GEMM shapes on the 16-bit MFMA and widens the rest
+    else:
+        cd = dispatch.compute_dtype(res_dtype)
     ops = [o.to(cd) for o in ops]
     lhs, out_str = _parse_subscripts(subscripts)
     terms = lhs.split(",")

@@ -53,13 +53,18 @@ def accumulation(mode: str):
 
 
 def dtype_code(dt: torch.dtype) -> int:
+    """Library dtype code of a launch on `dt` data (bfloat16/float16: tt_gemm only)."""
     if dt == torch.float64:
         return _lib.TT_F64_DD if _ACCUMULATION.get() == "dd" else _lib.TT_F64
     if dt == torch.float32:
         if _ACCUMULATION.get() == "dd":
             raise NotImplementedError("double-double accumulation needs float64 data")
         return _lib.TT_F32
-    raise NotImplementedError(f"HIP kernels compute in float32/float64, not {dt}")
+    if dt == torch.bfloat16:
+        return _lib.TT_BF16
+    if dt == torch.float16:
+        return _lib.TT_F16
+    raise NotImplementedError(f"HIP kernels compute in float32/float64 (bfloat16/float16 GEMMs), not {dt}")
 
 
 def _stream_ptr(device: torch.device) -> ctypes.c_void_p:
@@ -612,6 +617,39 @@ def contract_gemm(
 # ---------------------------------------------------------------------------
 # public entry: one or two operands
 # ---------------------------------------------------------------------------
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _contract_half(terms, out, tensors, alpha, beta, C, prefer_gemm, key):
+    """The in-place GEMM mapping of a 16-bit two-operand contraction, run on
+    the 16-bit MFMA GEMM, or None when the contraction needs anything else
+    (packing, a permuting pass, summed one-sided letters, K-splitting)."""
+    if len(tensors) != 2 or len(set(out)) != len(out):
+        return None
+    A, B = (Operand(t, x) for t, x in zip(terms, tensors))
+    la, lb, lo = set(A.letters), set(B.letters), set(out)
+    if any(c not in la and c not in lb for c in lo):
+        return None
+    if any(c not in lb and c not in lo for c in la) or any(c not in la and c not in lo for c in lb):
+        return None
+    kl = [c for c in A.letters if c in lb and c not in lo]
+    batch = [c for c in out if c in la and c in lb]
+    ml = [c for c in out if c in la and c not in lb]
+    nl = [c for c in out if c in lb and c not in la]
+    ext = {**A.ext, **B.ext}
+    M, N = _numel(ext[c] for c in ml), _numel(ext[c] for c in nl)
+    if not kl or not (prefer_gemm or (M >= 16 and N >= 16)):
+        return None
+    kl.sort(key=lambda c: -A.strd[c])
+    rec = _inplace_recipe(A, B, out, batch, ml, nl, kl, ext, tensors[0].dtype)
+    if rec is None:
+        return None
+    rec.split = 1  # slices would need a 16-bit reduction pass
+    if key is not None:
+        _RECIPES[key] = rec
+    return rec.run(A.t, B.t, alpha, beta, C)
+
+
 def contract(
     terms: list[str],
     out: str,
@@ -621,9 +659,13 @@ def contract(
     C: torch.Tensor | None = None,
     prefer_gemm: bool = False,
 ) -> torch.Tensor:
-    """einsum of one or two device tensors (same dtype, float32/float64).
+    """einsum of one or two device tensors (same dtype: float32/float64, or
+    bfloat16/float16 for contractions that map onto the GEMM in place).
 
     C (if given) is contiguous in the output's shape and enters as beta*C.
+    16-bit operands run on the 16-bit MFMA GEMM (fp32 accumulation) when the
+    contraction maps onto it without packing; otherwise they are widened to
+    float32 (exactly) and the result is rounded back to their dtype.
     """
     key = None
     if len(tensors) == 2:
@@ -634,6 +676,13 @@ def contract(
             return rec.run(a, b, alpha, beta, C)
         if len(_RECIPES) >= _RECIPES_MAX:
             _RECIPES.clear()
+    if tensors[0].dtype in _HALF:
+        res = _contract_half(terms, out, tensors, alpha, beta, C, prefer_gemm, key)
+        if res is not None:
+            return res
+        wide = contract(terms, out, [t.float() for t in tensors], alpha, beta, None if C is None else C.float(),
+                        prefer_gemm)
+        return wide.to(tensors[0].dtype)
     ops = [Operand(t, x) for t, x in zip(terms, tensors)]
     present = set().union(*[set(o.letters) for o in ops])
     if len(set(out)) != len(out):
