@@ -28,7 +28,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK = {"f64": 78.6e12, "f32": 157.3e12, "hbm": 8.0e12}
+PEAK = {"f64": 78.6e12, "f32": 157.3e12, "bf16": 2.5e15, "hbm": 8.0e12}
 
 
 def parse():
@@ -90,7 +90,7 @@ def timed_steady(torch, fn, steps, min_warm_s=0.3):
 
 
 def measured_peaks(torch, dev):
-    """Rates this device sustains in microbenchmarks: fp64/fp32 MFMA with no
+    """Rates this device sustains in microbenchmarks: fp64/fp32/bf16 MFMA with no
     memory traffic (tt_mfma_rate_probe) and a 1 GiB device-to-device copy
     (bytes read + written). The datasheet peaks assume the maximum clock;
     these are what the kernels' fractions can also be read against."""
@@ -100,10 +100,14 @@ def measured_peaks(torch, dev):
     st = torch.cuda.current_stream(dev).cuda_stream
     wgs = 1024
     out = {}
-    for key, code, dt in (("mfma_f64_TFLOPs", _lib.TT_F64, torch.float64), ("mfma_f32_TFLOPs", _lib.TT_F32, torch.float32)):
+    cases = (
+        ("mfma_f64_TFLOPs", _lib.TT_F64, torch.float64, 20000, 2048),
+        ("mfma_f32_TFLOPs", _lib.TT_F32, torch.float32, 40000, 2048),
+        ("mfma_bf16_TFLOPs", _lib.TT_BF16, torch.bfloat16, 40000, 16384),
+    )
+    for key, code, dt, iters, flop_per_mfma in cases:
         buf = torch.empty(wgs, dtype=dt, device=dev)
-        iters = 20000 if code == _lib.TT_F64 else 40000
-        flop = wgs * 4 * iters * 8 * 2048
+        flop = wgs * 4 * iters * 8 * flop_per_mfma
 
         def run():
             _lib.check(lib.tt_mfma_rate_probe(code, wgs, iters, buf.data_ptr(), st), "tt_mfma_rate_probe")
@@ -444,16 +448,25 @@ def bench_c2(torch, tt, dev, args):
         ("gemm4096", (4096, 4096), "ij,jk->ik", 2 * 4096**3),
         ("bmm64x512", (64, 512, 512), "bij,bjk->bik", 64 * 2 * 512**3),
     ):
-        for dt, key in ((torch.float64, "f64"), (torch.float32, "f32")):
+        for dt, key in ((torch.float64, "f64"), (torch.float32, "f32"), (torch.bfloat16, "bf16")):
             print(f"bench: c2 {name} {key}", file=sys.stderr, flush=True)
             hostA, hostB, hostC = (torch.randn(*shape, generator=g, dtype=torch.float64).to(dt) for _ in range(3))
             A, B, C = (x.to(dev) for x in (hostA, hostB, hostC))
             wall, ev_ms = timed_steady(torch, lambda: tt.einsum(sub, A, B, alpha=1.5, beta=0.5, out=C), max(5, args.steps))
+            # Library comparator on the same operands: hipBLASLt/rocBLAS through torch.
+            lib_fn = torch.addmm if A.dim() == 2 else torch.baddbmm
+            _, lib_ms = timed_steady(torch, lambda: lib_fn(C, A, B, beta=0.5, alpha=1.5), max(5, args.steps))
             out[f"{name}_{key}"] = {
                 "ms": round(ev_ms, 4),
                 "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
                 "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK[key], 4),
+                "torch_rocm_lib_TFLOP/s": round(flop / (lib_ms * 1e-3) / 1e12, 2),
             }
+            if key == "bf16":
+                # The reference has no bf16 config; this line times the 16-bit
+                # MFMA GEMM (einsum on bf16 operands), without a CPU leg.
+                del A, B, C, hostA, hostB, hostC
+                continue
             if not args.no_cpu:
                 from oracle import cpu_ref
 

@@ -185,10 +185,11 @@ int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape,
 
 /*
  * Measurement aid with no counterpart in the reference: `workgroups`
- * workgroups of 4 wavefronts each run `iters` rounds of 8 independent
- * 16x16x4 MFMA accumulator chains of `dtype` (TT_F32 or TT_F64) from register
- * operands, 8 * 2048 FLOP per wavefront per round, and write one value per
- * workgroup to out (device, `workgroups` elements of dtype). Timing it gives
+ * workgroups of 4 wavefronts each run `iters` rounds of 8 independent MFMA
+ * accumulator chains from register operands and write one value per
+ * workgroup to out (device, `workgroups` elements of dtype). TT_F32/TT_F64:
+ * 16x16x4 MFMA, 8 * 2048 FLOP per wavefront per round; TT_BF16/TT_F16:
+ * 16x16x32 MFMA with fp32 accumulators, 8 * 16384 FLOP per wavefront per round. Timing it gives
  * the MFMA rate the device sustains without memory traffic, the measured
  * peak that the benchmark reports next to the datasheet peak.
  */

@@ -87,3 +87,53 @@ def test_dtype_string_bf16_large(hip):
     assert got.dtype == torch.bfloat16
     want = (A.bfloat16().float() @ B.bfloat16().float()).bfloat16()
     assert normwise(got.float(), want.float()) <= 1e-2
+
+
+def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=False, seed=0):
+    """tt_gemm with TT_BF16/TT_F16 through engine.gemm against the float64
+    product of the same 16-bit inputs, rounded once to the 16-bit dtype."""
+    g = torch.Generator().manual_seed(seed)
+    dev = torch.device("cuda")
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    A = torch.randn(batch, a_rows, a_cols + pad, generator=g).to(dt)
+    B = torch.randn(batch, b_rows, b_cols + pad, generator=g).to(dt)
+    C = torch.randn(batch, M, N + pad, generator=g).to(dt)
+    opA = A[:, :, :a_cols].double().transpose(1, 2) if ta else A[:, :, :a_cols].double()
+    opB = B[:, :, :b_cols].double().transpose(1, 2) if tb else B[:, :, :b_cols].double()
+    ref = alpha * torch.bmm(opA, opB)
+    if with_c:
+        ref = ref + beta * C[:, :, :N].double()
+    ref = ref.to(dt)
+    Ad, Bd, Cd = A.to(dev), B.to(dev), C.to(dev)
+    D = Cd if alias else torch.full((batch, M, N + pad), float("nan"), dtype=dt, device=dev)
+    engine.gemm(
+        ta, tb, M, N, K,
+        Ad, a_cols + pad, a_rows * (a_cols + pad),
+        Bd, b_cols + pad, b_rows * (b_cols + pad),
+        D, N + pad, M * (N + pad), batch, alpha, beta,
+        Cd if with_c else None, N + pad, M * (N + pad),
+    )
+    torch.cuda.synchronize()
+    return normwise(D[:, :, :N].float().cpu(), ref.float())
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize(
+    "M,N,K,batch,pad",
+    [(1, 1, 1, 1, 0), (130, 136, 72, 1, 0), (264, 272, 96, 2, 0), (200, 150, 70, 2, 0), (96, 88, 40, 3, 3)],
+)
+def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
+    """Aligned leading dimensions (multiples of 8) take the 16-byte epilogue,
+    odd ones (pad 3) and ragged column blocks the element-wise one."""
+    assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
+    assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gemm16_d_aliases_c(hip, dt):
+    """D may alias C exactly (header contract): D = alpha * AB + beta * D."""
+    assert _gemm16_case(dt, False, True, 136, 264, 64, 2, 0.5, 2.0, True, alias=True, seed=3) <= BAR[dt]
+    assert _gemm16_case(dt, True, False, 100, 90, 33, 1, 0.5, 2.0, True, pad=1, alias=True, seed=4) <= BAR[dt]

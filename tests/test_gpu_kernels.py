@@ -166,3 +166,37 @@ def test_coltile_double_double(hip):
     with engine.accumulation("dd"):
         got = engine.contract(["ijk"], "k", [x.cuda()])
     assert torch.equal(got.cpu(), torch.full((96,), float(n // 2), dtype=torch.float64))
+
+
+@pytest.mark.parametrize(
+    "code,dt,expected_per_iter,tol",
+    [
+        # Lane 0 holds rows {0,4,8,12} (f64) or {0,1,2,3} (f32, 16-bit) of
+        # column 0 in each of 8 identical chains; operand of lane l is
+        # ((l & 7) + 1) * s and ((l >> 3 & 7) + 1) * s, s = 1e-6 (1e-3 for
+        # 16-bit), so per iteration D[i][0] = ((i & 7) + 1) * (1+3+5+7) s^2
+        # (times 8 for the 32-deep 16-bit MFMA).
+        (1, torch.float64, 8 * 12 * 16e-12, 1e-12),
+        (0, torch.float32, 8 * 10 * 16e-12, 1e-4),
+        (3, torch.bfloat16, 8 * 10 * 128e-6, 2e-2),
+        (4, torch.float16, 8 * 10 * 128e-6, 2e-2),
+    ],
+)
+def test_mfma_rate_probe_closed_form(hip, code, dt, expected_per_iter, tol):
+    """The measurement probe really issues `iters` rounds of its MFMA chains:
+    workgroup 0's value against the closed form of the operand pattern."""
+    from trntensor_amd.hip import _lib
+
+    lib = _lib.load()
+    out = torch.zeros(4, dtype=dt, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.tt_mfma_rate_probe(code, 4, 100, out.data_ptr(), st), "tt_mfma_rate_probe")
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    want = 100 * expected_per_iter
+    assert abs(got[0].item() - want) <= tol * want
+    assert torch.equal(got, got[:1].expand(4))
+    with pytest.raises(ValueError):
+        _lib.check(lib.tt_mfma_rate_probe(code, 0, 1, out.data_ptr(), st), "tt_mfma_rate_probe")
+    with pytest.raises(NotImplementedError):
+        _lib.check(lib.tt_mfma_rate_probe(2, 1, 1, out.data_ptr(), st), "tt_mfma_rate_probe")

@@ -194,6 +194,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
                 for (int j = 0; j < FN; ++j) acc[i][j] = Mfma16<T>::mma(fa[i], fb[j], acc[i][j]);
         }
     };
+    int64_t kt = 0;
     if (nk > 0) {
         if (nfull > 0) load(0, std::true_type{});
         else load(0, std::false_type{});
@@ -201,7 +202,6 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
         sb.store(bufB(0));
     }
     __syncthreads();
-    int64_t kt = 0;
     for (; kt + 1 < nfull; ++kt) {
         load((kt + 1) * BK, std::true_type{});
         compute(kt & 1);
@@ -210,6 +210,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
         sb.store(bufB((kt & 1) ^ 1));
         __syncthreads();
     }
+    // Buffer kt & 1 holds stage kt; the remaining stages load one ahead.
     for (; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
         if (more) load((kt + 1) * BK, std::false_type{});
@@ -222,26 +223,63 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
         __syncthreads();
     }
 
+    // Epilogue through LDS (free after the last barrier): each wave writes one
+    // 16-row slab of its tile as fp32 with alpha applied, then each lane
+    // finishes 8 consecutive columns of one row with a 16-byte load of C and a
+    // 16-byte store of D (element-wise at ragged or unaligned edges).
     const unsigned short* C = g.C ? static_cast<const unsigned short*>(g.C) + bat * g.sC : nullptr;
     unsigned short* D = static_cast<unsigned short*>(g.D) + bat * g.sD;
     const float alpha = (float)g.alpha;
     const float beta = (float)g.beta;
+    constexpr int SP = WN + 4;  // slab pitch in floats (16-byte multiple)
+    static_assert(4 * 16 * SP * sizeof(float) <= sizeof(lds), "epilogue slabs fit in the stage buffers");
+    float* slab = reinterpret_cast<float*>(lds) + wave * 16 * SP;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vout = a16(D) && g.ldd % 8 == 0 && (!C || (a16(C) && g.ldc % 8 == 0));
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int64_t col = n0 + wn0 + 16 * j + lrow;
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = m0 + wm0 + 16 * i + 4 * lg + r;
-                if (row < g.M && col < g.N) {
-                    float v = acc[i][j][r];
-                    if (g.alpha != 1.0) v = alpha * v;
-                    if (C) v = v + beta * to_f32<T>(C[row * g.ldc + col]);
-                    D[row * g.ldd + col] = from_f32<T>(v);
+                float v = acc[i][j][r];
+                if (g.alpha != 1.0) v = alpha * v;
+                slab[(4 * lg + r) * SP + 16 * j + lrow] = v;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < WN / 32; ++h) {
+            const int v = lane + 64 * h;
+            const int rr = v / (WN / 8), cb = v % (WN / 8);
+            const int64_t row = m0 + wm0 + 16 * i + rr;
+            const int64_t col = n0 + wn0 + 8 * cb;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(slab + rr * SP + 8 * cb);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(slab + rr * SP + 8 * cb + 4);
+            float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (row < g.M) {
+                if (vout && col + 8 <= g.N) {
+                    if (C) {
+                        const u16x8 c = *reinterpret_cast<const u16x8*>(C + row * g.ldc + col);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * to_f32<T>(c[e]);
+                    }
+                    u16x8 d;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d[e] = from_f32<T>(x[e]);
+                    *reinterpret_cast<u16x8*>(D + row * g.ldd + col) = d;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (col + e < g.N) {
+                            float y = x[e];
+                            if (C) y = y + beta * to_f32<T>(C[row * g.ldc + col + e]);
+                            D[row * g.ldd + col + e] = from_f32<T>(y);
+                        }
                 }
             }
         }
+        __syncthreads();
+    }
 }
 
 template <typename T, int BM, int BN, int BK>
