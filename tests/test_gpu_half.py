@@ -123,11 +123,25 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
 @pytest.mark.parametrize("tb", [False, True])
 @pytest.mark.parametrize(
     "M,N,K,batch,pad",
-    [(1, 1, 1, 1, 0), (130, 136, 72, 1, 0), (264, 272, 96, 2, 0), (200, 150, 70, 2, 0), (96, 88, 40, 3, 3)],
+    [
+        (1, 1, 1, 1, 0),
+        (130, 136, 72, 1, 0),
+        (264, 272, 96, 2, 0),
+        (200, 150, 70, 2, 0),
+        (96, 88, 40, 3, 3),
+        (300, 520, 100, 2, 0),
+        (512, 512, 512, 2, 0),
+        (264, 300, 129, 1, 3),
+        (520, 264, 1056, 1, 0),
+        (256, 512, 1024, 2, 0),
+    ],
 )
 def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     """Aligned leading dimensions (multiples of 8) take the 16-byte epilogue,
-    odd ones (pad 3) and ragged column blocks the element-wise one."""
+    odd ones (pad 3) and ragged column blocks the element-wise one. M, N >= 256
+    with aligned operands and K >= 1024 a multiple of 32 run whole 256 x 256
+    tiles on the direct-load kernel and the ragged strips on the register-staged
+    one (520 x 264 x 1056); 256 x 512 x 1024 is whole tiles only."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
 

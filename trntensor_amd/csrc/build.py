@@ -21,7 +21,19 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libtrntensor_hip.so")
-SOURCES = ["tt_abi.hip", "tt_dd.hip", "tt_gemm.hip", "tt_gemm16.hip", "tt_mp2.hip", "tt_probe.hip", "tt_strided.hip"]
+SOURCES = [
+    "tt_abi.hip",
+    "tt_dd.hip",
+    "tt_gemm.hip",
+    "tt_gemm16.hip",
+    "tt_gemm16_dma.hip",
+    "tt_mp2.hip",
+    "tt_probe.hip",
+    "tt_strided.hip",
+]
+# Sources whose MFMA accumulators belong in AGPRs (256 fp32 per lane): built
+# without the VGPR-accumulator option below.
+AGPR_SOURCES = {"tt_gemm16_dma.hip"}
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -58,7 +70,11 @@ def build(jobs: int = 4, verbose: bool = False, extra: list[str] | None = None) 
 
     def compile_one(src: str) -> str:
         obj = os.path.join(obj_dir, src.replace(".hip", ".o"))
-        cmd = [cc, *flags, "-c", os.path.join(HERE, src), "-o", obj]
+        fl = list(flags)
+        if src in AGPR_SOURCES:
+            i = fl.index("-amdgpu-mfma-vgpr-form")
+            del fl[i - 1 : i + 1]
+        cmd = [cc, *fl, "-c", os.path.join(HERE, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -304,8 +304,9 @@ int launch16(bool ta, bool tb, bool vec, GemmArgs& g, hipStream_t st) {
     return check_launch("tt_gemm (16-bit)");
 }
 
+// Register-staged kernel (any shape, alignment and K).
 template <typename T>
-int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
+int gemm16_staged(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     auto ok16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % 8 == 0 && g.ldb % 8 == 0;
     if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
@@ -316,6 +317,46 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 710-868; 128 x 256 x 64 (one workgroup per CU) 500.
     if (ta) return launch16<T, 256, 128, 32>(ta, tb, vec, g, st);
     return launch16<T, 128, 128, 64>(ta, tb, vec, g, st);
+}
+
+template <typename T>
+int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
+    auto ok16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    bool vec = ok16(g.A) && ok16(g.B) && g.lda % 8 == 0 && g.ldb % 8 == 0;
+    if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
+    // The direct-load kernel (one 256 x 256 workgroup per CU) needs K deep
+    // enough to amortise its prologue and epilogue: at 64 x 512^3 (K = 512) it
+    // measured 422 TFLOP/s against 456 for the register-staged kernel.
+    if (!vec || g.M < 256 || g.N < 256 || g.K < 1024 || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
+    // Whole 256 x 256 tiles by the direct-load kernel; the ragged row and
+    // column strips (if any) by the register-staged kernel on sub-matrices.
+    const int64_t Mi = g.M & ~(int64_t)255, Ni = g.N & ~(int64_t)255;
+    const unsigned short* A = static_cast<const unsigned short*>(g.A);
+    const unsigned short* B = static_cast<const unsigned short*>(g.B);
+    const unsigned short* C = static_cast<const unsigned short*>(g.C);
+    unsigned short* D = static_cast<unsigned short*>(g.D);
+    GemmArgs gi = g;
+    gi.M = Mi;
+    gi.N = Ni;
+    int rc = gemm16_dma_dispatch(std::is_same<T, __bf16>::value ? TT_BF16 : TT_F16, ta, tb, gi, st);
+    if (rc == TT_OK && Mi < g.M) {
+        GemmArgs ge = g;
+        ge.M = g.M - Mi;
+        ge.A = ta ? A + Mi : A + Mi * g.lda;
+        ge.C = C ? C + Mi * g.ldc : nullptr;
+        ge.D = D + Mi * g.ldd;
+        rc = gemm16_staged<T>(ta, tb, ge, st);
+    }
+    if (rc == TT_OK && Ni < g.N) {
+        GemmArgs ge = g;
+        ge.M = Mi;
+        ge.N = g.N - Ni;
+        ge.B = tb ? B + Ni * g.ldb : B + Ni;
+        ge.C = C ? C + Ni : nullptr;
+        ge.D = D + Ni;
+        rc = gemm16_staged<T>(ta, tb, ge, st);
+    }
+    return rc;
 }
 
 }  // namespace

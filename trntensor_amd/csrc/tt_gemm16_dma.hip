@@ -1,0 +1,325 @@
+// 16-bit GEMM, large-tile variant (dtype TT_BF16 / TT_F16 of tt_gemm when
+// M, N >= 256): the same arithmetic as gemm16_kernel (v_mfma_f32_16x16x32,
+// fp32 accumulators, alpha/beta in fp32, one rounding at the store) with
+//  - 256 x 256 workgroup tiles, four wavefronts of 128 x 128 (8 x 8 MFMA
+//    blocks; the 256 fp32 accumulators per lane live in AGPRs, so this file is
+//    built without the VGPR-accumulator option the other kernels use),
+//  - operands copied global -> LDS by the direct-load path
+//    (global_load_lds_dwordx4: no VGPR staging and no ds_write), 16 bytes per
+//    lane, one kilobyte of LDS per wavefront instruction,
+//  - a four-slot LDS ring of 32-deep stages with three stages in flight and
+//    one barrier per stage.
+// Per stage a wave issues 64 MFMAs (1024 MFMA cycles) against 16 KB of LDS
+// reads; the four waves together read 64 KB and the direct loads write 32 KB,
+// 96 bytes per clock of the LDS's 128 at the full MFMA rate.
+//
+// Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled so that each
+// 16-lane group of an MFMA operand read touches distinct banks):
+//   k-contiguous operand: row r (32 k = four pieces, 64 bytes) at r * 64,
+//     global piece p at position p ^ ((r >> 2) & 3);
+//   row-contiguous operand: k-row kr (256 rows = 32 pieces, 512 bytes) at
+//     kr * 512, global piece p at position p ^ (2 (kr & 3)).
+// Direct load q (0..15) of an operand fills bytes [1024 q, 1024 q + 1024);
+// wave w issues q = w, w + 4, w + 8, w + 12, and lane l writes position l.
+// Workgroups whose tile crosses the matrix edge, and the K tail, stage the
+// same layout through registers with bounds checks (zero fill).
+#include <type_traits>
+
+#include "tt_gemm.hpp"
+
+namespace tt {
+
+namespace {
+
+typedef __bf16 dbf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 df16x8 __attribute__((ext_vector_type(8)));
+typedef float df32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short du16x8 __attribute__((ext_vector_type(8)));
+typedef short ds16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDT = 256;                  // workgroup tile rows and columns
+constexpr int kDK = 32;                   // k per stage
+constexpr int kSlots = 4;                 // LDS ring slots (three stages in flight)
+constexpr int kOpBytes = kDT * kDK * 2;   // one operand's stage: 16 KB
+constexpr int kSlotBytes = 2 * kOpBytes;  // A, then B
+
+template <typename T>
+__device__ __forceinline__ df32x4 mma16(du16x8 a, du16x8 b, df32x4 c) {
+    if constexpr (std::is_same<T, __bf16>::value)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dbf16x8, a), __builtin_bit_cast(dbf16x8, b), c,
+                                                       0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(df16x8, a), __builtin_bit_cast(df16x8, b), c, 0,
+                                                      0, 0);
+}
+
+// The direct loads are issued as inline assembly (M0 = this instruction's LDS
+// kilobyte, then global_load_lds_dwordx4). Issued through the compiler
+// builtin, they are LDS writes the compiler cannot tell apart from any LDS
+// read, so every operand read would wait for all of them, including the
+// stages still in flight. As assembly they are invisible to the compiler; the
+// loop's own s_waitcnt and barrier order them against the reads, and the
+// compiler keeps tracking the reads themselves. Nothing else in the kernel
+// uses M0.
+__device__ __forceinline__ unsigned lds_off(const void* p) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma16(const unsigned short* g, unsigned lds_kilobyte) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_kilobyte)), "v"(g)
+                 : "memory", "m0");
+}
+
+template <bool KC>
+struct DStage {
+    // Row and k offsets (relative to the tile's row0 and the stage's k0) of
+    // the 8 elements lane `lane` of direct load q fetches.
+    __device__ __forceinline__ static void src(int q, int lane, int& row, int& k) {
+        if (KC) {
+            const int r = 16 * q + (lane >> 2);
+            row = r;
+            k = 8 * ((lane & 3) ^ ((r >> 2) & 3));
+        } else {
+            const int kr = 2 * q + (lane >> 5);
+            k = kr;
+            row = 8 * ((lane & 31) ^ (2 * (kr & 3)));
+        }
+    }
+
+    // Interior stage: this wave's four direct loads (all addresses in range).
+    __device__ __forceinline__ static void dma(const unsigned short* p, int64_t ld, int64_t row0, int64_t k0,
+                                               unsigned char* slot, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = wave + 4 * i;
+            int r, k;
+            src(q, lane, r, k);
+            const unsigned short* g = KC ? p + (row0 + r) * ld + k0 + k : p + (k0 + k) * ld + row0 + r;
+            dma16(g, lds_off(slot + 1024 * q));
+        }
+    }
+
+    // Edge or tail stage: the same layout through registers; elements outside
+    // rows x kdim are zero, and no address outside them is read.
+    __device__ __forceinline__ static void masked(const unsigned short* p, int64_t ld, int64_t row0, int64_t rows,
+                                                  int64_t k0, int64_t kdim, unsigned char* slot, int wave, int lane) {
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {
+            const int q = wave + 4 * i;
+            int r, k;
+            src(q, lane, r, k);
+            du16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t gr = row0 + r + (KC ? 0 : e);
+                const int64_t gk = k0 + k + (KC ? e : 0);
+                const bool ok = gr < rows && gk < kdim;
+                const unsigned short x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
+                v[e] = ok ? x : (unsigned short)0;
+            }
+            *reinterpret_cast<du16x8*>(slot + 1024 * q + 16 * lane) = v;
+        }
+    }
+
+    // This lane's MFMA operand for the 16 rows from rb: rows rb + (lane % 16),
+    // k 8 (lane / 16) .. 8 (lane / 16) + 7 (layout of the 16x16x32 MFMA).
+    __device__ __forceinline__ static du16x8 frag(const unsigned char* slot, int rb, int lane) {
+        if (KC) {
+            const int r = rb + (lane & 15), c = lane >> 4;
+            return *reinterpret_cast<const du16x8*>(slot + r * 64 + 16 * (c ^ ((r >> 2) & 3)));
+        }
+        // Transposing reads: within 16 lanes, lane 4 j + a supplies the 8-byte
+        // block of rows 4 b .. 4 b + 3 (b = rb / 4 + a) of k-row 8 g + 4 h + j,
+        // and lane 4 a + e receives element e of the blocks of lanes 4 j + a.
+        const int g = lane >> 4, j = (lane & 15) >> 2, a = lane & 3;
+        const int b = (rb >> 2) + a;
+        ds16x4 h[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kr = 8 * g + 4 * hh + j;
+            const int pos = (b >> 1) ^ (2 * (kr & 3));
+            typedef __attribute__((address_space(3))) ds16x4 lds_s16x4;
+            h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(slot + kr * 512 + 16 * pos + 8 * (b & 1)));
+        }
+        return du16x8{(unsigned short)h[0][0], (unsigned short)h[0][1], (unsigned short)h[0][2], (unsigned short)h[0][3],
+                      (unsigned short)h[1][0], (unsigned short)h[1][1], (unsigned short)h[1][2], (unsigned short)h[1][3]};
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ float dto_f32(unsigned short x) {
+    return (float)__builtin_bit_cast(T, x);
+}
+template <typename T>
+__device__ __forceinline__ unsigned short dfrom_f32(float x) {
+    return __builtin_bit_cast(unsigned short, (T)x);
+}
+
+template <typename T, bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
+    // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
+    typedef DStage<!TA> SA;
+    typedef DStage<TB> SB;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kSlots * kSlotBytes];
+
+    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t total = tiles * g.batch;
+    const int64_t id = xcd_remap(blockIdx.x, total);
+    const int64_t bat = id / tiles;
+    const int64_t t = id - bat * tiles;
+    constexpr int64_t GROUP = 4;
+    const int64_t grp = t / (GROUP * g.tiles_n);
+    const int64_t first_m = grp * GROUP;
+    const int64_t gsize = min(g.tiles_m - first_m, GROUP);
+    const int64_t rem = t - grp * GROUP * g.tiles_n;
+    const int64_t m0 = (first_m + rem % gsize) * kDT;
+    const int64_t n0 = (rem / gsize) * kDT;
+
+    const unsigned short* A = static_cast<const unsigned short*>(g.A) + bat * g.sA;
+    const unsigned short* B = static_cast<const unsigned short*>(g.B) + bat * g.sB;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave >> 1) * 128;
+    const int wn0 = (wave & 1) * 128;
+
+    // The host launches this kernel on whole tiles only (M, N multiples of
+    // 256 within the launch, K a multiple of 32, 16-byte aligned operands).
+    const int64_t nk = g.K / kDK;
+    auto slot = [&](int64_t s) __attribute__((always_inline)) -> unsigned char* { return lds + (int)(s & (kSlots - 1)) * kSlotBytes; };
+
+    df32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = df32x4{0, 0, 0, 0};
+
+    auto read = [&](du16x8 (&fa)[8], du16x8 (&fb)[8], int64_t s) __attribute__((always_inline)) {
+        const unsigned char* sl = slot(s);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fb[j] = SB::frag(sl + kOpBytes, wn0 + 16 * j, lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) fa[i] = SA::frag(sl, wm0 + 16 * i, lane);
+    };
+    auto mfma = [&](du16x8 (&fa)[8], du16x8 (&fb)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = mma16<T>(fa[i], fb[j], acc[i][j]);
+    };
+    // Make stage s readable by every wave, with `ahead` direct-loaded stages
+    // issued after it: this wave's direct loads of stage s are its oldest
+    // outstanding ones (vector-memory ops complete in order), so those of the
+    // later stages may stay in flight; lgkmcnt(0) also retires this wave's LDS
+    // reads of earlier stages and register-staged writes. A plain barrier then
+    // publishes stage s and frees the slot every wave has finished reading (a
+    // fenced barrier would also wait for the later stages).
+    auto ready = [&](int64_t ahead) __attribute__((always_inline)) {
+        // s_waitcnt immediate: vmcnt in bits 3:0 and 15:14, expcnt 6:4 (7: no
+        // wait), lgkmcnt 11:8.
+        if (ahead >= 3) __builtin_amdgcn_s_waitcnt(0x4078);       // vmcnt(24) lgkmcnt(0)
+        else if (ahead == 2) __builtin_amdgcn_s_waitcnt(0x4070);  // vmcnt(16) lgkmcnt(0)
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0078);  // vmcnt(8) lgkmcnt(0)
+        else __builtin_amdgcn_s_waitcnt(0x0070);                  // vmcnt(0) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+    };
+    // One stage at a time: after the barrier that publishes stage kt, stage
+    // kt + 3 is loaded into the slot stage kt - 1 used, then stage kt's
+    // operands are read and its MFMAs run.
+    auto dma = [&](int64_t s) __attribute__((always_inline)) {
+        unsigned char* sl = slot(s);
+        SA::dma(A, g.lda, m0, s * kDK, sl, wave, lane);
+        SB::dma(B, g.ldb, n0, s * kDK, sl + kOpBytes, wave, lane);
+    };
+    for (int64_t s = 0; s < kSlots - 1 && s < nk; ++s) dma(s);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // Stages issued after stage kt: those below min(nk, kt + 3).
+        ready(min<int64_t>(nk, kt + kSlots - 1) - (kt + 1));
+        if (kt + kSlots - 1 < nk) dma(kt + kSlots - 1);
+        du16x8 fa[8], fb[8];
+        read(fa, fb, kt);
+        mfma(fa, fb);
+    }
+    __syncthreads();
+
+    // Epilogue through LDS, one 16-row slab of the wave's tile at a time (fp32,
+    // alpha applied); each lane then finishes 8 consecutive columns of one row
+    // with a 16-byte load of C and a 16-byte store of D.
+    const unsigned short* C = g.C ? static_cast<const unsigned short*>(g.C) + bat * g.sC : nullptr;
+    unsigned short* D = static_cast<unsigned short*>(g.D) + bat * g.sD;
+    const float alpha = (float)g.alpha;
+    const float beta = (float)g.beta;
+    constexpr int SP = 128 + 4;  // slab pitch in floats
+    static_assert(4 * 16 * SP * sizeof(float) <= sizeof(lds), "epilogue slabs fit in the ring");
+    float* slab = reinterpret_cast<float*>(lds) + wave * 16 * SP;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vout = a16(D) && g.ldd % 8 == 0 && (!C || (a16(C) && g.ldc % 8 == 0));
+    const int lrow = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if (g.alpha != 1.0) v = alpha * v;
+                slab[(4 * lg + r) * SP + 16 * j + lrow] = v;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int v = lane + 64 * h;
+            const int rr = v >> 4, cb = v & 15;
+            const int64_t row = m0 + wm0 + 16 * i + rr;
+            const int64_t col = n0 + wn0 + 8 * cb;
+            const df32x4 lo = *reinterpret_cast<const df32x4*>(slab + rr * SP + 8 * cb);
+            const df32x4 hi = *reinterpret_cast<const df32x4*>(slab + rr * SP + 8 * cb + 4);
+            float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (row < g.M) {
+                if (vout && col + 8 <= g.N) {
+                    if (C) {
+                        const du16x8 c = *reinterpret_cast<const du16x8*>(C + row * g.ldc + col);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * dto_f32<T>(c[e]);
+                    }
+                    du16x8 d;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d[e] = dfrom_f32<T>(x[e]);
+                    *reinterpret_cast<du16x8*>(D + row * g.ldd + col) = d;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (col + e < g.N) {
+                            float y = x[e];
+                            if (C) y = y + beta * dto_f32<T>(C[row * g.ldc + col + e]);
+                            D[row * g.ldd + col + e] = dfrom_f32<T>(y);
+                        }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T>
+int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
+    g.tiles_m = (g.M + kDT - 1) / kDT;
+    g.tiles_n = (g.N + kDT - 1) / kDT;
+    const int64_t total = g.tiles_m * g.tiles_n * g.batch;
+    if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
+    const dim3 grid((unsigned)total), block(256);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false>), grid, block, 0, st, g);
+    if (!ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true>), grid, block, 0, st, g);
+    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false>), grid, block, 0, st, g);
+    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true>), grid, block, 0, st, g);
+    return check_launch("tt_gemm (16-bit, direct loads)");
+}
+
+}  // namespace
+
+int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
+    if (dtype == TT_BF16) return launch16_dma<__bf16>(ta, tb, g, st);
+    return launch16_dma<_Float16>(ta, tb, g, st);
+}
+
+}  // namespace tt
