@@ -93,6 +93,21 @@ __global__ __launch_bounds__(256) void gemm_dd_kernel(GemmArgs g) {
 
     double* D = static_cast<double*>(g.D) + bat * g.sD;
     const double* C = g.C ? static_cast<const double*>(g.C) + bat * g.sC : nullptr;
+    // All 16 C values are loaded (clamped addresses, branch-free) before the
+    // first store: D may alias C, so loads placed between stores could not be
+    // moved ahead of them and would each wait out a memory latency.
+    double cv[4][4];
+    if (C) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+                const bool ok = m < g.M && n < g.N;
+                const double c = C[ok ? m * g.ldc + n : 0];
+                cv[i][j] = ok ? c : 0.0;
+            }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t m = m0 + ty * 4 + i;
@@ -103,7 +118,7 @@ __global__ __launch_bounds__(256) void gemm_dd_kernel(GemmArgs g) {
             if (n >= g.N) continue;
             double v = acc[i][j].value();
             if (g.alpha != 1.0) v = g.alpha * v;
-            if (C) v = v + g.beta * C[m * g.ldc + n];
+            if (C) v = v + g.beta * cv[i][j];
             D[m * g.ldd + n] = v;
         }
     }

@@ -254,12 +254,31 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 
     // Store epilogue: D = alpha * acc (+ beta * C), masked at the matrix edge.
+    // D may alias C, so the compiler cannot move a load of C past a store of
+    // D: loaded element by element, every element would wait out a full
+    // memory latency before its store. Each 16-row block's C values are
+    // therefore loaded (from clamped addresses, branch-free) before any of
+    // its stores, which keeps FN * 4 loads in flight together.
     const T alpha = (T)g.alpha;
     const T beta = (T)g.beta;
     const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
     T* D = static_cast<T*>(g.D) + bat * g.sD;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+        T cv[FN][4];
+        if (C) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int64_t col = n0 + wn0 + 16 * j + col_l;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
+                    const bool ok = row < g.M && col < g.N;
+                    const T c = C[ok ? row * g.ldc + col : 0];
+                    cv[j][r] = ok ? c : T(0);
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int64_t col = n0 + wn0 + 16 * j + col_l;
@@ -269,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
                 if (row < g.M && col < g.N) {
                     T v = acc[i][j][r];
                     if (g.alpha != 1.0) v = alpha * v;
-                    if (C) v = v + beta * C[row * g.ldc + col];
+                    if (C) v = v + beta * cv[j][r];
                     D[row * g.ldd + col] = v;
                 }
             }

@@ -238,6 +238,20 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
     const bool vout = a16(D) && g.ldd % 8 == 0 && (!C || (a16(C) && g.ldc % 8 == 0));
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+        // This slab's C chunks are loaded before any of its stores (and before the
+        // slab exchange, whose barrier then covers their latency): D may
+        // alias C, so the compiler cannot move a load of C past a store of D,
+        // and chunk-by-chunk loads would each wait out a full memory latency.
+        u16x8 cc[WN / 32];
+#pragma unroll
+        for (int h = 0; h < WN / 32; ++h) {
+            const int v = lane + 64 * h;
+            const int rr = v / (WN / 8), cb = v % (WN / 8);
+            const int64_t row = m0 + wm0 + 16 * i + rr;
+            const int64_t col = n0 + wn0 + 8 * cb;
+            cc[h] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (C && vout && row < g.M && col + 8 <= g.N) cc[h] = *reinterpret_cast<const u16x8*>(C + row * g.ldc + col);
+        }
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -259,9 +273,8 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
             if (row < g.M) {
                 if (vout && col + 8 <= g.N) {
                     if (C) {
-                        const u16x8 c = *reinterpret_cast<const u16x8*>(C + row * g.ldc + col);
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * to_f32<T>(c[e]);
+                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * to_f32<T>(cc[h][e]);
                     }
                     u16x8 d;
 #pragma unroll

@@ -257,6 +257,20 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     const int lrow = lane & 15, lg = lane >> 4;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+        // This slab's C chunks are loaded before any of its stores (and before the
+        // slab exchange, whose barrier then covers their latency): D may
+        // alias C, so the compiler cannot move a load of C past a store of D,
+        // and chunk-by-chunk loads would each wait out a full memory latency.
+        du16x8 cc[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int v = lane + 64 * h;
+            const int rr = v >> 4, cb = v & 15;
+            const int64_t row = m0 + wm0 + 16 * i + rr;
+            const int64_t col = n0 + wn0 + 8 * cb;
+            cc[h] = du16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (C && vout && row < g.M && col + 8 <= g.N) cc[h] = *reinterpret_cast<const du16x8*>(C + row * g.ldc + col);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -278,9 +292,8 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
             if (row < g.M) {
                 if (vout && col + 8 <= g.N) {
                     if (C) {
-                        const du16x8 c = *reinterpret_cast<const du16x8*>(C + row * g.ldc + col);
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * dto_f32<T>(c[e]);
+                        for (int e = 0; e < 8; ++e) x[e] = x[e] + beta * dto_f32<T>(cc[h][e]);
                     }
                     du16x8 d;
 #pragma unroll
