@@ -100,6 +100,23 @@ class TestGemm:
         bound = 1.5 * (U * np.abs(exact) + gamma(n) ** 2 * scale) + 2 * U * (np.abs(1.5 * exact) + np.abs(want))
         assert np.all(err <= bound)
 
+    def test_d_aliases_c(self, hip):
+        """D may alias C exactly (header contract): all of a thread's C values
+        are read before its first store, so D = alpha * AB + beta * D holds."""
+        from trntensor_amd.hip import engine
+
+        gen = torch.Generator().manual_seed(11)
+        A, B, C = rand(gen, 70, 45), rand(gen, 45, 66), rand(gen, 70, 66)
+        Cd = C.cuda()
+        with engine.accumulation("dd"):
+            engine.gemm(False, False, 70, 66, 45, A.cuda(), 45, 0, B.cuda(), 66, 0, Cd, 66, 0, 1, 1.5, -0.25, Cd, 66, 0)
+        torch.cuda.synchronize()
+        exact, scale, n = brute.einsum_exact("ij,jk->ik", A.numpy(), B.numpy())
+        want = 1.5 * exact - 0.25 * C.numpy()
+        err = np.abs(Cd.cpu().numpy() - want)
+        bound = 1.5 * (U * np.abs(exact) + gamma(n) ** 2 * scale) + 2 * U * (np.abs(1.5 * exact) + np.abs(want))
+        assert np.all(err <= bound)
+
     def test_float32_operands(self, hip):
         """float32 inputs: exact products of their float64 values, result rounded
         to float64 and then to float32 (within one float32 ulp of the exact value)."""

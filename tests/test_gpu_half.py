@@ -151,3 +151,6 @@ def test_gemm16_d_aliases_c(hip, dt):
     """D may alias C exactly (header contract): D = alpha * AB + beta * D."""
     assert _gemm16_case(dt, False, True, 136, 264, 64, 2, 0.5, 2.0, True, alias=True, seed=3) <= BAR[dt]
     assert _gemm16_case(dt, True, False, 100, 90, 33, 1, 0.5, 2.0, True, pad=1, alias=True, seed=4) <= BAR[dt]
+    # the direct-load 256 x 256 kernel (whole tiles) and its ragged strips
+    assert _gemm16_case(dt, False, False, 256, 512, 1024, 2, 0.5, 2.0, True, alias=True, seed=5) <= BAR[dt]
+    assert _gemm16_case(dt, True, True, 520, 264, 1056, 1, 0.5, 2.0, True, alias=True, seed=6) <= BAR[dt]

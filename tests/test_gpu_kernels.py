@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float64: 1e-12, torch.float32: 1e-5}
 
 
-def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed=0):
+def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed=0, alias=False):
     from trntensor_amd.hip import engine
 
     g = torch.Generator().manual_seed(seed)
@@ -36,7 +36,7 @@ def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed
     if with_c:
         ref = ref + beta * C
     Ad, Bd, Cd = A.to(dev, dt), B.to(dev, dt), C.to(dev, dt)
-    D = torch.full((batch, M, N), float("nan"), dtype=dt, device=dev)
+    D = Cd if alias else torch.full((batch, M, N), float("nan"), dtype=dt, device=dev)
     engine.gemm(
         ta, tb, M, N, K,
         Ad, a_cols + pad, a_rows * (a_cols + pad),
@@ -65,6 +65,23 @@ def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
     # odd leading dimensions disable the 16-byte vector path
     assert _gemm_case(hip, dt, False, True, 70, 90, 50, 3, 1.5, 0.5, True, pad=pad, seed=1) <= TOL[dt]
     assert _gemm_case(hip, dt, True, False, 130, 65, 40, 2, -0.75, 2.0, True, pad=pad, seed=2) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize(
+    "ta,tb,M,N,K,batch",
+    [
+        (False, False, 64, 300, 70, 2),  # 64 x 128 tiles (M <= 64)
+        (True, False, 200, 150, 40, 3),  # 64 x 128 (fp64 batched, K <= 1024) / 128 x 128 (fp32)
+        (False, True, 300, 50, 90, 1),  # 256 x 64 tiles (N <= 64)
+        (True, True, 257, 300, 129, 1),  # 128 x 128 tiles, ragged edges
+    ],
+)
+def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
+    """D may alias C exactly (header contract): D = alpha * op(A) op(B) + beta * D.
+    Each row block's C values are loaded before its stores, so every element is
+    read before it is overwritten."""
+    assert _gemm_case(hip, dt, ta, tb, M, N, K, batch, 1.5, 0.5, True, seed=M + N, alias=True) <= TOL[dt]
 
 
 def test_gemm_k_zero_is_beta_c(hip):
