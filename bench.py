@@ -285,6 +285,12 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK["f64"], 4),
             "traffic": traffic_from_profiles("mp2_energy_kernel<double>"),
+            # The byte counters see every L2 miss; the DRAM-request counter
+            # (TCC_EA0_RDREQ_DRAM) reads the same 33 GB, so MALL hits are
+            # included. B (197 MB) fits the 256 MB MALL: the panel re-reads of
+            # the 64 x 64 work units are served there.
+            "traffic_scope": "L2 misses (MALL hits + HBM); B fits the 256 MB MALL",
+            "algorithmic_bytes": int(B.numel() * B.element_size() + (eo.numel() + ev.numel()) * 8),
             "event_ms_per_launch": round(ev_ms, 4),
         },
     }
