@@ -116,7 +116,7 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
         cd = res_dtype  # the engine runs GEMM shapes on the 16-bit MFMA and widens the rest
     else:
         cd = dispatch.compute_dtype(res_dtype)
-    ops = [o.to(cd) for o in ops]
+    ops = [o if o.dtype == cd else o.to(cd) for o in ops]
     lhs, out_str = _parse_subscripts(subscripts)
     terms = lhs.split(",")
 
@@ -131,7 +131,9 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
         res = engine.contract(
             terms, out_str, ops, alpha, beta, C, prefer_gemm=plan.strategy in ("matmul", "bmm")
         )
-    return res.to(res_dtype).to(orig)
+    if res.dtype != res_dtype:
+        res = res.to(res_dtype)
+    return res if res.device == orig else res.to(orig)
 
 
 def _result_shape(terms, out_str, ops) -> list[int]:

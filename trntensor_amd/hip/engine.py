@@ -67,12 +67,23 @@ def dtype_code(dt: torch.dtype) -> int:
     raise NotImplementedError(f"HIP kernels compute in float32/float64 (bfloat16/float16 GEMMs), not {dt}")
 
 
-def _stream_ptr(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+# Raw handle of torch's current stream on a device index (what
+# torch.cuda.current_stream(device).cuda_stream returns, without building a
+# Stream object: a few microseconds per launch on small contractions).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+def _stream_ptr(device: torch.device) -> int:
+    """torch's current stream on `device`, the stream every launch is enqueued on."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    """Device address of `t` (ctypes passes an int for a void* argument), or NULL."""
+    return None if t is None else t.data_ptr()
 
 
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
@@ -239,8 +250,8 @@ def strided_contract(
     rb = _lib.i64_array(d[2] for d in red_dims)
     wsb = lib.tt_strided_contract_workspace_bytes(code, len(out_dims), oshape, len(red_dims), rshape)
     ws = _workspace(wsb, D.device)
-    a_ptr = ctypes.c_void_p(A.data_ptr() + a_off * es)
-    b_ptr = None if B is None else ctypes.c_void_p(B.data_ptr() + b_off * es)
+    a_ptr = A.data_ptr() + a_off * es
+    b_ptr = None if B is None else B.data_ptr() + b_off * es
     st = lib.tt_strided_contract(
         code,
         len(out_dims),
@@ -310,10 +321,10 @@ def gemm(
         N,
         K,
         float(alpha),
-        ctypes.c_void_p(A.data_ptr() + a_off * es),
+        A.data_ptr() + a_off * es,
         lda,
         sA,
-        ctypes.c_void_p(B.data_ptr() + b_off * es),
+        B.data_ptr() + b_off * es,
         ldb,
         sB,
         float(beta),
