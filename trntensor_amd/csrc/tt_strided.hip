@@ -112,6 +112,40 @@ struct Acc<double, true> : Dot2 {
     }
 };
 
+// acc += sum over r = r0, r0 + step, ... < r1 of A[oa + a_roff(r)] (* B[ob + b_roff(r)]),
+// in that order. The loads of four consecutive terms are issued before their
+// sums (the order of the sums is unchanged, so results are bit-identical to a
+// plain loop): each thread keeps four loads in flight instead of one on these
+// memory-bound loops ('ijk->i' and 'ijk->k' on 1 GiB: +13%).
+template <typename T, bool DD>
+__device__ __forceinline__ void reduce_range(Acc<T, DD>& acc, const T* __restrict__ A, const T* __restrict__ B,
+                                             int64_t oa, int64_t ob, const Dims& red, int64_t r0, int64_t r1,
+                                             int64_t step) {
+    int64_t r = r0;
+    for (; r + 3 * step < r1; r += 4 * step) {
+        T x[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int64_t ra, rb;
+            decode((uint32_t)(r + u * step), red, ra, rb);
+            x[u] = A[oa + ra];
+            if (B) y[u] = B[ob + rb];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (B) acc.add_prod(x[u], y[u]);
+            else acc.add(x[u]);
+        }
+    }
+    for (; r < r1; r += step) {
+        int64_t ra, rb;
+        decode((uint32_t)r, red, ra, rb);
+        const T x = A[oa + ra];
+        if (B) acc.add_prod(x, B[ob + rb]);
+        else acc.add(x);
+    }
+}
+
 template <typename T, bool DD>
 __device__ __forceinline__ T finish(const StridedArgs& g, int64_t o, const Acc<T, DD>& acc) {
     T v = acc.value();
@@ -129,13 +163,7 @@ __global__ __launch_bounds__(256) void strided_per_output_kernel(StridedArgs g) 
         int64_t oa, ob;
         decode((uint32_t)o, g.out, oa, ob);
         Acc<T, DD> acc;
-        for (int64_t r = 0; r < g.n_red; ++r) {
-            int64_t ra, rb;
-            decode((uint32_t)r, g.red, ra, rb);
-            const T x = A[oa + ra];
-            if (B) acc.add_prod(x, B[ob + rb]);
-            else acc.add(x);
-        }
+        reduce_range<T, DD>(acc, A, B, oa, ob, g.red, 0, g.n_red, 1);
         D[o] = finish<T, DD>(g, o, acc);
     }
 }
@@ -151,14 +179,7 @@ __global__ __launch_bounds__(256) void strided_per_block_kernel(StridedArgs g) {
     int64_t oa, ob;
     decode((uint32_t)o, g.out, oa, ob);
     Acc<T, DD> acc;
-    const int64_t step = g.nsplit * 256;
-    for (int64_t r = s * 256 + threadIdx.x; r < g.n_red; r += step) {
-        int64_t ra, rb;
-        decode((uint32_t)r, g.red, ra, rb);
-        const T x = A[oa + ra];
-        if (B) acc.add_prod(x, B[ob + rb]);
-        else acc.add(x);
-    }
+    reduce_range<T, DD>(acc, A, B, oa, ob, g.red, s * 256 + threadIdx.x, g.n_red, g.nsplit * 256);
     // Block sum: wavefront shuffles, then the four wave totals in order.
     acc.wave_reduce();
     if ((threadIdx.x & 63) == 0) acc.put(red, threadIdx.x >> 6);
@@ -201,13 +222,7 @@ __global__ __launch_bounds__(256) void strided_coltile_kernel(StridedArgs g) {
     const int64_t r0 = (int64_t)blockIdx.y * chunk;
     const int64_t r1 = min(g.n_red, r0 + chunk);
     Acc<T, DD> acc;
-    for (int64_t r = r0; r < r1; ++r) {
-        int64_t ra, rb;
-        decode((uint32_t)r, g.red, ra, rb);
-        const T x = A[oa + ra];
-        if (B) acc.add_prod(x, B[ob + rb]);
-        else acc.add(x);
-    }
+    reduce_range<T, DD>(acc, A, B, oa, ob, g.red, r0, r1, 1);
     if (g.nsplit == 1) static_cast<T*>(g.D)[o] = finish<T, DD>(g, o, acc);
     else acc.store_partial(g.partial, (int64_t)blockIdx.y * g.n_out + o, g.nsplit * g.n_out);
 }
