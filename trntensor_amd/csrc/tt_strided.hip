@@ -251,24 +251,45 @@ __global__ __launch_bounds__(256) void strided_transpose_kernel(StridedArgs g, T
     const T* A = static_cast<const T*>(g.A);
     const int lo = threadIdx.x & 63;
     const int hi = threadIdx.x >> 6;
-#pragma unroll 4
+    // All 16 loads of a thread are issued before its LDS stores, branch-free
+    // (an element outside the tensor loads the batch's first element, which
+    // always exists, into a tile cell that is never stored): loads inside
+    // per-element bounds branches were each followed by a wait, one memory
+    // latency per element.
+    T x[16];
+#pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int ul = hi + 4 * i;
         const int64_t u = u0 + ul, v = v0 + lo;
-        if (u < t.U && v < t.V) tile[ul][lo] = A[za + u * t.sa_u + v * t.sa_v];
+        const bool ok = u < t.U && v < t.V;
+        x[i] = A[ok ? za + u * t.sa_u + v * t.sa_v : za];
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tile[hi + 4 * i][lo] = x[i];
     __syncthreads();
     T* D = static_cast<T*>(g.D);
-#pragma unroll 4
+    const T* C = static_cast<const T*>(g.C);
+    // The beta term's C values are likewise loaded before the first store (D
+    // may alias C element for element).
+    T c[16];
+    if (C) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int vl = hi + 4 * i;
+            const int64_t u = u0 + lo, v = v0 + vl;
+            const bool ok = u < t.U && v < t.V;
+            c[i] = C[ok ? zd + v * t.sd_v + u : zd];
+        }
+    }
+#pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int vl = hi + 4 * i;
         const int64_t u = u0 + lo, v = v0 + vl;
         if (u < t.U && v < t.V) {
-            const int64_t o = zd + v * t.sd_v + u;
-            T x = tile[lo][vl];
-            if (g.alpha != 1.0) x = (T)g.alpha * x;
-            if (g.C) x = x + (T)g.beta * static_cast<const T*>(g.C)[o];
-            D[o] = x;
+            T y = tile[lo][vl];
+            if (g.alpha != 1.0) y = (T)g.alpha * y;
+            if (C) y = y + (T)g.beta * c[i];
+            D[zd + v * t.sd_v + u] = y;
         }
     }
 }
