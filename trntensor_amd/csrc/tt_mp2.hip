@@ -293,20 +293,35 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     const T* ev = static_cast<const T*>(g.ev);
     const T eij = eo[i] + eo[j];
     const bool mirror = (p != q);
+    // The lane's orbital energies are all loaded first, branch-free (a row
+    // outside the block loads ev[0]; its terms are skipped below): loads
+    // inside the per-element bounds branches each waited out a latency.
+    T e_bv[2], e_av[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int cb = wc + 16 * b + (lane & 15);
+        e_bv[b] = ev[cb < rows_q ? q * kMp2Tile + cb : 0];
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int ra = wr + 16 * a + MF::row(lg, r);
+            e_av[a][r] = ev[ra < rows_p ? p * kMp2Tile + ra : 0];
+        }
     double sum = 0.0;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const int cb = wc + 16 * b + (lane & 15);
-        const int vb = q * kMp2Tile + cb;
         const bool okb = cb < rows_q;
-        const T e_b = okb ? ev[vb] : T(0);
+        const T e_b = e_bv[b];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int ra = wr + 16 * a + MF::row(lg, r);
                 if (okb && ra < rows_p) {
-                    const T e_a = ev[p * kMp2Tile + ra];
+                    const T e_a = e_av[a][r];
                     const T x = X[a][b][r];
                     const T y = ymode == 1 ? x : Y[a][b][r];
                     const T d_ab = (eij - e_a) - e_b;
