@@ -239,6 +239,20 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
         du16x8 fa[8], fb[8];
         read(fa, fb, kt);
         mfma(fa, fb);
+        // Software pipeline for the scheduler: the B fragments and the first
+        // two A fragments are read up front, then each row's 8 MFMAs are
+        // followed by the read of the A fragment two rows ahead, so every
+        // read has a row of MFMAs to land in (left alone, the scheduler put
+        // each A read right before its row, behind a full wait).
+        constexpr int RA = TA ? 2 : 1;  // LDS read instructions per A fragment
+        constexpr int RB = TB ? 1 : 2;  // per B fragment
+        __builtin_amdgcn_sched_group_barrier(0x100, 8 * RB + 2 * RA, 0);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
     }
     __syncthreads();
 
