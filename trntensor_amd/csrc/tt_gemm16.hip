@@ -338,9 +338,13 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % 8 == 0 && g.ldb % 8 == 0;
     if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
     // The direct-load kernel (one 256 x 256 workgroup per CU) needs K deep
-    // enough to amortise its prologue and epilogue: at 64 x 512^3 (K = 512) it
-    // measured 422 TFLOP/s against 456 for the register-staged kernel.
-    if (!vec || g.M < 256 || g.N < 256 || g.K < 1024 || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
+    // enough to amortise its prologue and epilogue. With A k-contiguous it is
+    // the faster from K = 512 (bf16, 64 x 512^3: 482 against 460 TFLOP/s;
+    // 4 x 2048^2 x 768: 641 against 600); with A row-contiguous the 256 x 128
+    // register-staged tile stays ahead there (507 against 536, 640 against 687).
+    // At K = 256 it loses in every layout (327 against 347-395).
+    const int64_t kmin = ta ? 1024 : 512;
+    if (!vec || g.M < 256 || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
     // Whole 256 x 256 tiles by the direct-load kernel; the ragged row and
     // column strips (if any) by the register-staged kernel on sub-matrices.
     const int64_t Mi = g.M & ~(int64_t)255, Ni = g.N & ~(int64_t)255;
