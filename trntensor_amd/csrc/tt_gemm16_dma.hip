@@ -87,16 +87,17 @@ struct DStage {
         }
     }
 
-    // Interior stage: this wave's four direct loads (all addresses in range).
+    // Interior stage: this wave's four direct loads (all addresses in range);
+    // slot_off is the stage's LDS byte address, uniform across the wave.
     __device__ __forceinline__ static void dma(const unsigned short* p, int64_t ld, int64_t row0, int64_t k0,
-                                               unsigned char* slot, int wave, int lane) {
+                                               unsigned slot_off, int wave, int lane) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int q = wave + 4 * i;
             int r, k;
             src(q, lane, r, k);
             const unsigned short* g = KC ? p + (row0 + r) * ld + k0 + k : p + (k0 + k) * ld + row0 + r;
-            dma16(g, lds_off(slot + 1024 * q));
+            dma16(g, slot_off + 1024 * q);
         }
     }
 
@@ -179,7 +180,9 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     const unsigned short* A = static_cast<const unsigned short*>(g.A) + bat * g.sA;
     const unsigned short* B = static_cast<const unsigned short*>(g.B) + bat * g.sB;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // Uniform by construction; as a scalar it keeps every direct load's LDS
+    // offset (M0) in scalar registers.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm0 = (wave >> 1) * 128;
     const int wn0 = (wave & 1) * 128;
 
@@ -226,10 +229,13 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     // One stage at a time: after the barrier that publishes stage kt, stage
     // kt + 3 is loaded into the slot stage kt - 1 used, then stage kt's
     // operands are read and its MFMAs run.
+    // Slot offsets are integer LDS addresses: converting a generic pointer per
+    // load cost a null check and a vector-to-scalar move on every one.
+    const unsigned lds0 = lds_off(lds);
     auto dma = [&](int64_t s) __attribute__((always_inline)) {
-        unsigned char* sl = slot(s);
-        SA::dma(A, g.lda, m0, s * kDK, sl, wave, lane);
-        SB::dma(B, g.ldb, n0, s * kDK, sl + kOpBytes, wave, lane);
+        const unsigned so = lds0 + (unsigned)(s & (kSlots - 1)) * kSlotBytes;
+        SA::dma(A, g.lda, m0, s * kDK, so, wave, lane);
+        SB::dma(B, g.ldb, n0, s * kDK, so + kOpBytes, wave, lane);
     };
     for (int64_t s = 0; s < kSlots - 1 && s < nk; ++s) dma(s);
     for (int64_t kt = 0; kt < nk; ++kt) {
