@@ -339,10 +339,11 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
     // The direct-load kernel (one 256 x 256 workgroup per CU) needs K deep
     // enough to amortise its prologue and epilogue. With A k-contiguous it is
-    // the faster from K = 512 (bf16, 64 x 512^3: 482 against 460 TFLOP/s;
-    // 4 x 2048^2 x 768: 641 against 600); with A row-contiguous the 256 x 128
-    // register-staged tile stays ahead there (507 against 536, 640 against 687).
-    // At K = 256 it loses in every layout (327 against 347-395).
+    // level or ahead from K = 512 (bf16, 64 x 512^3: 517-520 against 508-513
+    // TFLOP/s; 4 x 2048^2 x 768: 642-653 against 612-621); with A
+    // row-contiguous the 256 x 128 register-staged tile stays ahead there
+    // (507 against 536, 640 against 687). At K = 256 it loses in every layout
+    // (327 against 347-395).
     const int64_t kmin = ta ? 1024 : 512;
     if (!vec || g.M < 256 || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
     // Whole 256 x 256 tiles by the direct-load kernel; the ragged row and
