@@ -11,12 +11,14 @@
 //    one barrier per stage.
 // Per stage a wave issues 64 MFMAs (1024 MFMA cycles) against 16 KB of LDS
 // reads; the four waves together read 64 KB and the direct loads write 32 KB,
-// 96 bytes per clock of the LDS's 128 at the full MFMA rate.
+// 96 bytes per clock at the full MFMA rate, of the 256 the LDS serves when
+// every 16-lane quarter of a 16-byte access covers one 256-byte run.
 //
 // Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled so that each
 // 16-lane group of an MFMA operand read touches distinct banks):
 //   k-contiguous operand: row r (32 k = four pieces, 64 bytes) at r * 64,
-//     global piece p at position p ^ ((r >> 2) & 3);
+//     global piece p at position p ^ ((r >> 2) & 3); B of the TT layout
+//     instead piece-major per 16-row block (see DStage);
 //   row-contiguous operand: k-row kr (256 rows = 32 pieces, 512 bytes) at
 //     kr * 512, global piece p at position p ^ (2 (kr & 3)).
 // Direct load q (0..15) of an operand fills bytes [1024 q, 1024 q + 1024);
@@ -71,12 +73,23 @@ __device__ __forceinline__ void dma16(const unsigned short* g, unsigned lds_kilo
                  : "memory", "m0");
 }
 
-template <bool KC>
+// PM (k-contiguous operands only): piece-major 16-row blocks. Block b (rows
+// 16 b .. 16 b + 15) fills one direct load's kilobyte as [piece][row], so each
+// 16-lane quarter of a fragment read covers one 256-byte run, which the LDS
+// serves in one pass (the swizzled [row][piece] layout takes two). Each
+// quarter of a direct load then reads 16 rows instead of 4, which costs more
+// address work. Measured at 4096^3 bf16: B piece-major with A row-contiguous
+// (TT) 1054-1057 -> 1106 TFLOP/s; with A k-contiguous too (NT) 1083 -> 1059-1078;
+// A piece-major (NN) 1060 -> 969.
+template <bool KC, bool PM = false>
 struct DStage {
     // Row and k offsets (relative to the tile's row0 and the stage's k0) of
     // the 8 elements lane `lane` of direct load q fetches.
     __device__ __forceinline__ static void src(int q, int lane, int& row, int& k) {
-        if (KC) {
+        if (KC && PM) {
+            row = 16 * q + (lane & 15);
+            k = 8 * (lane >> 4);
+        } else if (KC) {
             const int r = 16 * q + (lane >> 2);
             row = r;
             k = 8 * ((lane & 3) ^ ((r >> 2) & 3));
@@ -126,6 +139,7 @@ struct DStage {
     // This lane's MFMA operand for the 16 rows from rb: rows rb + (lane % 16),
     // k 8 (lane / 16) .. 8 (lane / 16) + 7 (layout of the 16x16x32 MFMA).
     __device__ __forceinline__ static du16x8 frag(const unsigned char* slot, int rb, int lane) {
+        if (KC && PM) return *reinterpret_cast<const du16x8*>(slot + (rb >> 4) * 1024 + (lane >> 4) * 256 + (lane & 15) * 16);
         if (KC) {
             const int r = rb + (lane & 15), c = lane >> 4;
             return *reinterpret_cast<const du16x8*>(slot + r * 64 + 16 * (c ^ ((r >> 2) & 3)));
@@ -161,7 +175,7 @@ template <typename T, bool TA, bool TB>
 __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
     typedef DStage<!TA> SA;
-    typedef DStage<TB> SB;
+    typedef DStage<TB, TA> SB;  // piece-major B only for TT (see DStage)
     __shared__ __attribute__((aligned(1024))) unsigned char lds[kSlots * kSlotBytes];
 
     const int64_t tiles = g.tiles_m * g.tiles_n;
