@@ -1,18 +1,23 @@
 // 16-bit GEMM, large-tile variant (dtype TT_BF16 / TT_F16 of tt_gemm when
 // M, N >= 256): the same arithmetic as gemm16_kernel (v_mfma_f32_16x16x32,
 // fp32 accumulators, alpha/beta in fp32, one rounding at the store) with
-//  - 256 x 256 workgroup tiles, four wavefronts of 128 x 128 (8 x 8 MFMA
-//    blocks; the 256 fp32 accumulators per lane live in AGPRs, so this file is
-//    built without the VGPR-accumulator option the other kernels use),
+//  - BM x 256 workgroup tiles, four wavefronts of (BM / 2) x 128;
+//    BM = 256: 8 x 8 MFMA blocks per wave, 256 fp32 accumulators per lane
+//    (AGPRs; this file is built without the VGPR-accumulator option the other
+//    kernels use), one workgroup per CU; BM = 128: 4 x 8 blocks, two
+//    workgroups per CU, whose independent barriers let one workgroup's MFMAs
+//    run while the other waits,
 //  - operands copied global -> LDS by the direct-load path
 //    (global_load_lds_dwordx4: no VGPR staging and no ds_write), 16 bytes per
 //    lane, one kilobyte of LDS per wavefront instruction,
-//  - a four-slot LDS ring of 32-deep stages with three stages in flight and
-//    one barrier per stage.
-// Per stage a wave issues 64 MFMAs (1024 MFMA cycles) against 16 KB of LDS
-// reads; the four waves together read 64 KB and the direct loads write 32 KB,
-// 96 bytes per clock at the full MFMA rate, of the 256 the LDS serves when
-// every 16-lane quarter of a 16-byte access covers one 256-byte run.
+//  - an LDS ring of 32-deep stages, one barrier per stage: four slots with
+//    three stages in flight (BM = 256, 128 KB) or three slots with two in
+//    flight (BM = 128, 72 KB).
+// BM = 256: per stage a wave issues 64 MFMAs (1024 MFMA cycles) against 16 KB
+// of LDS reads; the four waves together read 64 KB and the direct loads write
+// 32 KB, 96 bytes per clock at the full MFMA rate, of the 256 the LDS serves
+// when every 16-lane quarter of a 16-byte access covers one 256-byte run
+// (BM = 128 moves half as many bytes again per MFMA).
 //
 // Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled so that each
 // 16-lane group of an MFMA operand read touches distinct banks):
@@ -21,8 +26,8 @@
 //     instead piece-major per 16-row block (see DStage);
 //   row-contiguous operand: k-row kr (256 rows = 32 pieces, 512 bytes) at
 //     kr * 512, global piece p at position p ^ (2 (kr & 3)).
-// Direct load q (0..15) of an operand fills bytes [1024 q, 1024 q + 1024);
-// wave w issues q = w, w + 4, w + 8, w + 12, and lane l writes position l.
+// Direct load q (0..ROWS/16 - 1) of an operand fills bytes [1024 q, 1024 q +
+// 1024); wave w issues q = w, w + 4, ..., and lane l writes position l.
 // Workgroups whose tile crosses the matrix edge, and the K tail, stage the
 // same layout through registers with bounds checks (zero fill).
 #include <type_traits>
@@ -81,8 +86,9 @@ __device__ __forceinline__ void dma16(const unsigned short* g, unsigned lds_kilo
 // address work. Measured at 4096^3 bf16: B piece-major with A row-contiguous
 // (TT) 1054-1057 -> 1106 TFLOP/s; with A k-contiguous too (NT) 1083 -> 1059-1078;
 // A piece-major (NN) 1060 -> 969.
-template <bool KC, bool PM = false>
+template <bool KC, bool PM = false, int ROWS = 256>
 struct DStage {
+    static_assert(ROWS == 256 || (ROWS == 128 && KC && !PM), "128-row stages: swizzled k-contiguous layout only");
     // Row and k offsets (relative to the tile's row0 and the stage's k0) of
     // the 8 elements lane `lane` of direct load q fetches.
     __device__ __forceinline__ static void src(int q, int lane, int& row, int& k) {
@@ -105,7 +111,7 @@ struct DStage {
     __device__ __forceinline__ static void dma(const unsigned short* p, int64_t ld, int64_t row0, int64_t k0,
                                                unsigned slot_off, int wave, int lane) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < ROWS / 64; ++i) {
             const int q = wave + 4 * i;
             int r, k;
             src(q, lane, r, k);
@@ -119,7 +125,7 @@ struct DStage {
     __device__ __forceinline__ static void masked(const unsigned short* p, int64_t ld, int64_t row0, int64_t rows,
                                                   int64_t k0, int64_t kdim, unsigned char* slot, int wave, int lane) {
 #pragma unroll 1
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < ROWS / 64; ++i) {
             const int q = wave + 4 * i;
             int r, k;
             src(q, lane, r, k);
@@ -171,12 +177,18 @@ __device__ __forceinline__ unsigned short dfrom_f32(float x) {
     return __builtin_bit_cast(unsigned short, (T)x);
 }
 
-template <typename T, bool TA, bool TB>
-__global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
+template <typename T, bool TA, bool TB, int BM>
+__global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(GemmArgs g) {
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
-    typedef DStage<!TA> SA;
+    typedef DStage<!TA, false, BM> SA;
     typedef DStage<TB, TA> SB;  // piece-major B only for TT (see DStage)
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[kSlots * kSlotBytes];
+    static_assert(BM == 256 || (BM == 128 && !TA), "128-row tiles: A k-contiguous only");
+    constexpr int FM = BM / 32;                 // 16-row MFMA blocks per wave
+    constexpr int NS = BM == 256 ? kSlots : 3;  // ring slots
+    constexpr int AB = BM * kDK * 2;            // A bytes per stage
+    constexpr int SB_ = AB + kOpBytes;          // slot bytes
+    constexpr int DPW = BM / 64 + 4;            // direct loads per wave per stage
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NS * SB_];
 
     const int64_t tiles = g.tiles_m * g.tiles_n;
     const int64_t total = tiles * g.batch;
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     const int64_t first_m = grp * GROUP;
     const int64_t gsize = min(g.tiles_m - first_m, GROUP);
     const int64_t rem = t - grp * GROUP * g.tiles_n;
-    const int64_t m0 = (first_m + rem % gsize) * kDT;
+    const int64_t m0 = (first_m + rem % gsize) * BM;
     const int64_t n0 = (rem / gsize) * kDT;
 
     const unsigned short* A = static_cast<const unsigned short*>(g.A) + bat * g.sA;
@@ -197,30 +209,30 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     // Uniform by construction; as a scalar it keeps every direct load's LDS
     // offset (M0) in scalar registers.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm0 = (wave >> 1) * 128;
+    const int wm0 = (wave >> 1) * (BM / 2);
     const int wn0 = (wave & 1) * 128;
 
     // The host launches this kernel on whole tiles only (M, N multiples of
     // 256 within the launch, K a multiple of 32, 16-byte aligned operands).
     const int64_t nk = g.K / kDK;
-    auto slot = [&](int64_t s) __attribute__((always_inline)) -> unsigned char* { return lds + (int)(s & (kSlots - 1)) * kSlotBytes; };
+    auto slot = [&](int64_t s) __attribute__((always_inline)) -> unsigned char* { return lds + ((int)s % NS) * SB_; };
 
-    df32x4 acc[8][8];
+    df32x4 acc[FM][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = df32x4{0, 0, 0, 0};
 
-    auto read = [&](du16x8 (&fa)[8], du16x8 (&fb)[8], int64_t s) __attribute__((always_inline)) {
+    auto read = [&](du16x8 (&fa)[FM], du16x8 (&fb)[8], int64_t s) __attribute__((always_inline)) {
         const unsigned char* sl = slot(s);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) fb[j] = SB::frag(sl + kOpBytes, wn0 + 16 * j, lane);
+        for (int j = 0; j < 8; ++j) fb[j] = SB::frag(sl + AB, wn0 + 16 * j, lane);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) fa[i] = SA::frag(sl, wm0 + 16 * i, lane);
+        for (int i = 0; i < FM; ++i) fa[i] = SA::frag(sl, wm0 + 16 * i, lane);
     };
-    auto mfma = [&](du16x8 (&fa)[8], du16x8 (&fb)[8]) __attribute__((always_inline)) {
+    auto mfma = [&](du16x8 (&fa)[FM], du16x8 (&fb)[8]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[i][j] = mma16<T>(fa[i], fb[j], acc[i][j]);
     };
@@ -234,10 +246,11 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     auto ready = [&](int64_t ahead) __attribute__((always_inline)) {
         // s_waitcnt immediate: vmcnt in bits 3:0 and 15:14, expcnt 6:4 (7: no
         // wait), lgkmcnt 11:8.
-        if (ahead >= 3) __builtin_amdgcn_s_waitcnt(0x4078);       // vmcnt(24) lgkmcnt(0)
-        else if (ahead == 2) __builtin_amdgcn_s_waitcnt(0x4070);  // vmcnt(16) lgkmcnt(0)
-        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0078);  // vmcnt(8) lgkmcnt(0)
-        else __builtin_amdgcn_s_waitcnt(0x0070);                  // vmcnt(0) lgkmcnt(0)
+        constexpr auto imm = [](int vm) { return (vm & 15) | ((vm >> 4) << 14) | 0x70; };  // lgkmcnt(0), no expcnt wait
+        if (ahead >= 3) __builtin_amdgcn_s_waitcnt(imm(3 * DPW));
+        else if (ahead == 2) __builtin_amdgcn_s_waitcnt(imm(2 * DPW));
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(imm(DPW));
+        else __builtin_amdgcn_s_waitcnt(imm(0));
         asm volatile("s_barrier" ::: "memory");
     };
     // One stage at a time: after the barrier that publishes stage kt, stage
@@ -247,16 +260,16 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     // load cost a null check and a vector-to-scalar move on every one.
     const unsigned lds0 = lds_off(lds);
     auto dma = [&](int64_t s) __attribute__((always_inline)) {
-        const unsigned so = lds0 + (unsigned)(s & (kSlots - 1)) * kSlotBytes;
+        const unsigned so = lds0 + (unsigned)((int)s % NS) * SB_;
         SA::dma(A, g.lda, m0, s * kDK, so, wave, lane);
-        SB::dma(B, g.ldb, n0, s * kDK, so + kOpBytes, wave, lane);
+        SB::dma(B, g.ldb, n0, s * kDK, so + AB, wave, lane);
     };
-    for (int64_t s = 0; s < kSlots - 1 && s < nk; ++s) dma(s);
+    for (int64_t s = 0; s < NS - 1 && s < nk; ++s) dma(s);
     for (int64_t kt = 0; kt < nk; ++kt) {
-        // Stages issued after stage kt: those below min(nk, kt + 3).
-        ready(min<int64_t>(nk, kt + kSlots - 1) - (kt + 1));
-        if (kt + kSlots - 1 < nk) dma(kt + kSlots - 1);
-        du16x8 fa[8], fb[8];
+        // Stages issued after stage kt: those below min(nk, kt + NS - 1).
+        ready(min<int64_t>(nk, kt + NS - 1) - (kt + 1));
+        if (kt + NS - 1 < nk) dma(kt + NS - 1);
+        du16x8 fa[FM], fb[8];
         read(fa, fb, kt);
         mfma(fa, fb);
         // Software pipeline for the scheduler: the B fragments and the first
@@ -268,7 +281,7 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
         constexpr int RB = TB ? 1 : 2;  // per B fragment
         __builtin_amdgcn_sched_group_barrier(0x100, 8 * RB + 2 * RA, 0);
 #pragma unroll
-        for (int i = 0; i < 6; ++i) {
+        for (int i = 0; i < FM - 2; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
         }
@@ -290,7 +303,7 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
     const bool vout = a16(D) && g.ldd % 8 == 0 && (!C || (a16(C) && g.ldc % 8 == 0));
     const int lrow = lane & 15, lg = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < FM; ++i) {
         // This slab's C chunks are loaded before any of its stores (and before the
         // slab exchange, whose barrier then covers their latency): D may
         // alias C, so the compiler cannot move a load of C past a store of D,
@@ -350,15 +363,23 @@ __global__ __launch_bounds__(256) void gemm16_dma_kernel(GemmArgs g) {
 
 template <typename T>
 int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
-    g.tiles_m = (g.M + kDT - 1) / kDT;
+    // Tile height, measured at bf16 (TFLOP/s, 128 against 256 rows): NN 4096^3
+    // 1104 against 1029, 4096^2 x 1024 855 against 704-740, 64 x 512^3 661-666
+    // against 517; NT 4096^2 x 1024 797 against 734-748, x 2048 931 against
+    // 905-917, x 3072 987-989 against 980-992, 4096^3 1013 against 1043. The
+    // 128-row tile covers A k-contiguous only (NN, NT).
+    const bool rows128 = !ta && (!tb || g.K <= 2048);
+    const int bm = rows128 ? 128 : 256;
+    g.tiles_m = (g.M + bm - 1) / bm;
     g.tiles_n = (g.N + kDT - 1) / kDT;
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const dim3 grid((unsigned)total), block(256);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false>), grid, block, 0, st, g);
-    if (!ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true>), grid, block, 0, st, g);
-    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false>), grid, block, 0, st, g);
-    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true>), grid, block, 0, st, g);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false, 128>), grid, block, 0, st, g);
+    if (!ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128>), grid, block, 0, st, g);
+    if (!ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 256>), grid, block, 0, st, g);
+    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 256>), grid, block, 0, st, g);
+    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 256>), grid, block, 0, st, g);
     return check_launch("tt_gemm (16-bit, direct loads)");
 }
 
