@@ -142,12 +142,11 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
 def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     """Aligned leading dimensions (multiples of 8) take the 16-byte epilogue,
     odd ones (pad 3) and ragged column blocks the element-wise one. M, N >= 256
-    with aligned operands and K a multiple of 32, at least 256 (A k-contiguous)
-    or 1024 (A row-contiguous), run whole tiles on the direct-load kernel and
-    the ragged strips on the register-staged one (520 x 264 x 1056,
-    384 x 256 x 512). Its tiles are 128 x 256 for NN and for NT up to
-    K = 2048 (256 x 256 x 256, 512^3, 256 x 512 x 1024), 256 x 256 otherwise
-    (NT at 256 x 256 x 2560, TN and TT from K = 1024)."""
+    with aligned operands and K a multiple of 32, at least 256, run whole
+    tiles on the direct-load kernel and the ragged strips on the
+    register-staged one (520 x 264 x 1056, 384 x 256 x 512). Its tiles are
+    128 x 256 for NN and TN, for NT up to K = 2048 and for TT up to K = 1024,
+    256 x 256 otherwise (NT and TT at 256 x 256 x 2560)."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
 

@@ -338,13 +338,12 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % 8 == 0 && g.ldb % 8 == 0;
     if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
     // The direct-load kernel (one 256 x 256 workgroup per CU) needs K deep
-    // enough to amortise its prologue and epilogue. With A k-contiguous (its
-    // 128 x 256 tiles) it is ahead from K = 256 (bf16, 64 x 512^2 x 256:
-    // 370-409 against 338-346 TFLOP/s; 64 x 512^3: 601-666 against 508-513);
-    // with A row-contiguous the 256 x 128 register-staged tile stays ahead
-    // below K = 1024 (507 against 536 at 64 x 512^3, 640 against 687 at
-    // 4 x 2048^2 x 768).
-    const int64_t kmin = ta ? 1024 : 256;
+    // enough to amortise its prologue and epilogue. With its 128 x 256 tiles
+    // it is level or ahead from K = 256 in every layout (bf16, 64 x 512^2 x 256:
+    // NN 370-374 against 338-342 TFLOP/s, NT 389-409 against 338-346, TN
+    // 398-403 against 400-401, TT 419 against 392-396; 64 x 512^3: 588-669
+    // against 508-562).
+    const int64_t kmin = 256;
     if (!vec || g.M < 256 || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
     // Whole 256 x 256 tiles by the direct-load kernel; the ragged row and
     // column strips (if any) by the register-staged kernel on sub-matrices.

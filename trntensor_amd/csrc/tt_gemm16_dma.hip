@@ -24,8 +24,8 @@
 //   k-contiguous operand: row r (32 k = four pieces, 64 bytes) at r * 64,
 //     global piece p at position p ^ ((r >> 2) & 3); B of the TT layout
 //     instead piece-major per 16-row block (see DStage);
-//   row-contiguous operand: k-row kr (256 rows = 32 pieces, 512 bytes) at
-//     kr * 512, global piece p at position p ^ (2 (kr & 3)).
+//   row-contiguous operand: k-row kr (ROWS rows = ROWS / 8 pieces, 2 ROWS
+//     bytes) at kr * 2 ROWS, global piece p at position p ^ (2 (kr & 3)).
 // Direct load q (0..ROWS/16 - 1) of an operand fills bytes [1024 q, 1024 q +
 // 1024); wave w issues q = w, w + 4, ..., and lane l writes position l.
 // Workgroups whose tile crosses the matrix edge, and the K tail, stage the
@@ -88,7 +88,8 @@ __device__ __forceinline__ void dma16(const unsigned short* g, unsigned lds_kilo
 // A piece-major (NN) 1060 -> 969.
 template <bool KC, bool PM = false, int ROWS = 256>
 struct DStage {
-    static_assert(ROWS == 256 || (ROWS == 128 && KC && !PM), "128-row stages: swizzled k-contiguous layout only");
+    static_assert(ROWS == 256 || (ROWS == 128 && !PM), "128-row stages: swizzled layouts only");
+    static constexpr int KRB = ROWS * 2;  // bytes per k-row of a row-contiguous stage
     // Row and k offsets (relative to the tile's row0 and the stage's k0) of
     // the 8 elements lane `lane` of direct load q fetches.
     __device__ __forceinline__ static void src(int q, int lane, int& row, int& k) {
@@ -100,9 +101,9 @@ struct DStage {
             row = r;
             k = 8 * ((lane & 3) ^ ((r >> 2) & 3));
         } else {
-            const int kr = 2 * q + (lane >> 5);
+            const int kr = (1024 / KRB) * q + lane / (KRB / 16);
             k = kr;
-            row = 8 * ((lane & 31) ^ (2 * (kr & 3)));
+            row = 8 * ((lane % (KRB / 16)) ^ (2 * (kr & 3)));
         }
     }
 
@@ -161,7 +162,7 @@ struct DStage {
             const int kr = 8 * g + 4 * hh + j;
             const int pos = (b >> 1) ^ (2 * (kr & 3));
             typedef __attribute__((address_space(3))) ds16x4 lds_s16x4;
-            h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(slot + kr * 512 + 16 * pos + 8 * (b & 1)));
+            h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(slot + kr * KRB + 16 * pos + 8 * (b & 1)));
         }
         return du16x8{(unsigned short)h[0][0], (unsigned short)h[0][1], (unsigned short)h[0][2], (unsigned short)h[0][3],
                       (unsigned short)h[1][0], (unsigned short)h[1][1], (unsigned short)h[1][2], (unsigned short)h[1][3]};
@@ -182,7 +183,6 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
     typedef DStage<!TA, false, BM> SA;
     typedef DStage<TB, TA> SB;  // piece-major B only for TT (see DStage)
-    static_assert(BM == 256 || (BM == 128 && !TA), "128-row tiles: A k-contiguous only");
     constexpr int FM = BM / 32;                 // 16-row MFMA blocks per wave
     constexpr int NS = BM == 256 ? kSlots : 3;  // ring slots
     constexpr int AB = BM * kDK * 2;            // A bytes per stage
@@ -364,11 +364,13 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
 template <typename T>
 int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // Tile height, measured at bf16 (TFLOP/s, 128 against 256 rows): NN 4096^3
-    // 1104 against 1029, 4096^2 x 1024 855 against 704-740, 64 x 512^3 661-666
-    // against 517; NT 4096^2 x 1024 797 against 734-748, x 2048 931 against
-    // 905-917, x 3072 987-989 against 980-992, 4096^3 1013 against 1043. The
-    // 128-row tile covers A k-contiguous only (NN, NT).
-    const bool rows128 = !ta && (!tb || g.K <= 2048);
+    // 1104 against 1029, 4096^2 x 1024 855 against 704-740; TN 4096^3
+    // 1169-1172 against 1030-1034, x 1024 902-911 against 725-732; NT
+    // 4096^2 x 1024 797 against 734-748, x 2048 931 against 905-917, x 3072
+    // 987-989 against 980-992, 4096^3 1013 against 1043; TT x 1024 763-767
+    // against 747-754, x 2048 881-897 against 944-946, 4096^3 929-946 against
+    // 1070-1077.
+    const bool rows128 = !tb || g.K <= (ta ? 1024 : 2048);
     const int bm = rows128 ? 128 : 256;
     g.tiles_m = (g.M + bm - 1) / bm;
     g.tiles_n = (g.N + kDT - 1) / kDT;
@@ -378,8 +380,9 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false, 128>), grid, block, 0, st, g);
     if (!ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128>), grid, block, 0, st, g);
     if (!ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 256>), grid, block, 0, st, g);
-    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 256>), grid, block, 0, st, g);
-    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 256>), grid, block, 0, st, g);
+    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 128>), grid, block, 0, st, g);
+    if (ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128>), grid, block, 0, st, g);
+    if (ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 256>), grid, block, 0, st, g);
     return check_launch("tt_gemm (16-bit, direct loads)");
 }
 
