@@ -145,8 +145,7 @@ def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     with aligned operands and K a multiple of 32, at least 256, run whole
     tiles on the direct-load kernel and the ragged strips on the
     register-staged one (520 x 264 x 1056, 384 x 256 x 512). Its tiles are
-    128 x 256 for NN and TN, for NT up to K = 2048 and for TT up to K = 1024,
-    256 x 256 otherwise (NT and TT at 256 x 256 x 2560)."""
+    128 x 256, except 256 x 256 for NT beyond K = 2048 (256 x 256 x 2560)."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
 

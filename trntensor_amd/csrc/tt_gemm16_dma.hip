@@ -22,8 +22,7 @@
 // Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled so that each
 // 16-lane group of an MFMA operand read touches distinct banks):
 //   k-contiguous operand: row r (32 k = four pieces, 64 bytes) at r * 64,
-//     global piece p at position p ^ ((r >> 2) & 3); B of the TT layout
-//     instead piece-major per 16-row block (see DStage);
+//     global piece p at position p ^ ((r >> 2) & 3);
 //   row-contiguous operand: k-row kr (ROWS rows = ROWS / 8 pieces, 2 ROWS
 //     bytes) at kr * 2 ROWS, global piece p at position p ^ (2 (kr & 3)).
 // Direct load q (0..ROWS/16 - 1) of an operand fills bytes [1024 q, 1024 q +
@@ -78,25 +77,14 @@ __device__ __forceinline__ void dma16(const unsigned short* g, unsigned lds_kilo
                  : "memory", "m0");
 }
 
-// PM (k-contiguous operands only): piece-major 16-row blocks. Block b (rows
-// 16 b .. 16 b + 15) fills one direct load's kilobyte as [piece][row], so each
-// 16-lane quarter of a fragment read covers one 256-byte run, which the LDS
-// serves in one pass (the swizzled [row][piece] layout takes two). Each
-// quarter of a direct load then reads 16 rows instead of 4, which costs more
-// address work. Measured at 4096^3 bf16: B piece-major with A row-contiguous
-// (TT) 1054-1057 -> 1106 TFLOP/s; with A k-contiguous too (NT) 1083 -> 1059-1078;
-// A piece-major (NN) 1060 -> 969.
-template <bool KC, bool PM = false, int ROWS = 256>
+template <bool KC, int ROWS = 256>
 struct DStage {
-    static_assert(ROWS == 256 || (ROWS == 128 && !PM), "128-row stages: swizzled layouts only");
+    static_assert(ROWS == 256 || ROWS == 128, "stage rows");
     static constexpr int KRB = ROWS * 2;  // bytes per k-row of a row-contiguous stage
     // Row and k offsets (relative to the tile's row0 and the stage's k0) of
     // the 8 elements lane `lane` of direct load q fetches.
     __device__ __forceinline__ static void src(int q, int lane, int& row, int& k) {
-        if (KC && PM) {
-            row = 16 * q + (lane & 15);
-            k = 8 * (lane >> 4);
-        } else if (KC) {
+        if (KC) {
             const int r = 16 * q + (lane >> 2);
             row = r;
             k = 8 * ((lane & 3) ^ ((r >> 2) & 3));
@@ -146,7 +134,6 @@ struct DStage {
     // This lane's MFMA operand for the 16 rows from rb: rows rb + (lane % 16),
     // k 8 (lane / 16) .. 8 (lane / 16) + 7 (layout of the 16x16x32 MFMA).
     __device__ __forceinline__ static du16x8 frag(const unsigned char* slot, int rb, int lane) {
-        if (KC && PM) return *reinterpret_cast<const du16x8*>(slot + (rb >> 4) * 1024 + (lane >> 4) * 256 + (lane & 15) * 16);
         if (KC) {
             const int r = rb + (lane & 15), c = lane >> 4;
             return *reinterpret_cast<const du16x8*>(slot + r * 64 + 16 * (c ^ ((r >> 2) & 3)));
@@ -181,8 +168,8 @@ __device__ __forceinline__ unsigned short dfrom_f32(float x) {
 template <typename T, bool TA, bool TB, int BM>
 __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(GemmArgs g) {
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
-    typedef DStage<!TA, false, BM> SA;
-    typedef DStage<TB, TA> SB;  // piece-major B only for TT (see DStage)
+    typedef DStage<!TA, BM> SA;
+    typedef DStage<TB> SB;
     constexpr int FM = BM / 32;                 // 16-row MFMA blocks per wave
     constexpr int NS = BM == 256 ? kSlots : 3;  // ring slots
     constexpr int AB = BM * kDK * 2;            // A bytes per stage
@@ -367,10 +354,10 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 1104 against 1029, 4096^2 x 1024 855 against 704-740; TN 4096^3
     // 1169-1172 against 1030-1034, x 1024 902-911 against 725-732; NT
     // 4096^2 x 1024 797 against 734-748, x 2048 931 against 905-917, x 3072
-    // 987-989 against 980-992, 4096^3 1013 against 1043; TT x 1024 763-767
-    // against 747-754, x 2048 881-897 against 944-946, 4096^3 929-946 against
-    // 1070-1077.
-    const bool rows128 = !tb || g.K <= (ta ? 1024 : 2048);
+    // 987-989 against 980-992, 4096^3 1013 against 1043; TT x 1024 846-850
+    // against 747-754, x 2048 993-995 against 921-946, 4096^3 1088-1091
+    // against 1070-1077.
+    const bool rows128 = ta || !tb || g.K <= 2048;
     const int bm = rows128 ? 128 : 256;
     g.tiles_m = (g.M + bm - 1) / bm;
     g.tiles_n = (g.N + kDT - 1) / kDT;
@@ -381,8 +368,7 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (!ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128>), grid, block, 0, st, g);
     if (!ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 256>), grid, block, 0, st, g);
     if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 128>), grid, block, 0, st, g);
-    if (ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128>), grid, block, 0, st, g);
-    if (ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 256>), grid, block, 0, st, g);
+    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128>), grid, block, 0, st, g);
     return check_launch("tt_gemm (16-bit, direct loads)");
 }
 
