@@ -137,6 +137,7 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
         (256, 256, 256, 2, 0),
         (384, 256, 512, 1, 0),
         (256, 256, 2560, 1, 0),
+        (200, 300, 512, 2, 0),
     ],
 )
 def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
@@ -144,7 +145,7 @@ def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     odd ones (pad 3) and ragged column blocks the element-wise one. M, N >= 256
     with aligned operands and K a multiple of 32, at least 256, run whole
     tiles on the direct-load kernel and the ragged strips on the
-    register-staged one (520 x 264 x 1056, 384 x 256 x 512). Its tiles are
+    register-staged one (520 x 264 x 1056, 200 x 300 x 512). Its tiles are
     128 x 256, except 256 x 256 for NT beyond K = 2048 (256 x 256 x 2560)."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]

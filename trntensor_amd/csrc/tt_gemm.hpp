@@ -34,9 +34,11 @@ int gemm_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
 int gemm_dd_dispatch(bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // 16-bit GEMM (dtype TT_BF16 / TT_F16) on the 16x16x32 MFMA; same arguments.
 int gemm16_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
-// Its 256 x 256 direct-load variant: 16-byte aligned operands (A, B, lda,
-// ldb and batch strides multiples of 8 elements), M and N >= 256.
+// Its direct-load variant: 16-byte aligned operands (A, B, lda, ldb and
+// batch strides multiples of 8 elements), whole tiles of gemm16_dma_rows
+// rows by 256 columns, K a multiple of 32.
 int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
+int gemm16_dma_rows(bool ta, bool tb, int64_t K);
 // Dot epilogue; writes one double per workgroup to g.partial and returns the
 // number of workgroups in *nparts.
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);

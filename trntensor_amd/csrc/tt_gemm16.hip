@@ -337,17 +337,18 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     auto ok16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % 8 == 0 && g.ldb % 8 == 0;
     if (g.batch > 1) vec = vec && g.sA % 8 == 0 && g.sB % 8 == 0;
-    // The direct-load kernel (one 256 x 256 workgroup per CU) needs K deep
-    // enough to amortise its prologue and epilogue. With its 128 x 256 tiles
+    // The direct-load kernel needs K deep enough to amortise its prologue and
+    // epilogue. With its 128 x 256 tiles
     // it is level or ahead from K = 256 in every layout (bf16, 64 x 512^2 x 256:
     // NN 370-374 against 338-342 TFLOP/s, NT 389-409 against 338-346, TN
     // 398-403 against 400-401, TT 419 against 392-396; 64 x 512^3: 588-669
     // against 508-562).
     const int64_t kmin = 256;
-    if (!vec || g.M < 256 || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
-    // Whole 256 x 256 tiles by the direct-load kernel; the ragged row and
+    const int64_t bm = gemm16_dma_rows(ta, tb, g.K);
+    if (!vec || g.M < bm || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
+    // Whole bm x 256 tiles by the direct-load kernel; the ragged row and
     // column strips (if any) by the register-staged kernel on sub-matrices.
-    const int64_t Mi = g.M & ~(int64_t)255, Ni = g.N & ~(int64_t)255;
+    const int64_t Mi = g.M & ~(bm - 1), Ni = g.N & ~(int64_t)255;
     const unsigned short* A = static_cast<const unsigned short*>(g.A);
     const unsigned short* B = static_cast<const unsigned short*>(g.B);
     const unsigned short* C = static_cast<const unsigned short*>(g.C);

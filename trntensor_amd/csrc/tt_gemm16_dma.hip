@@ -357,8 +357,8 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 987-989 against 980-992, 4096^3 1013 against 1043; TT x 1024 846-850
     // against 747-754, x 2048 993-995 against 921-946, 4096^3 1088-1091
     // against 1070-1077.
-    const bool rows128 = ta || !tb || g.K <= 2048;
-    const int bm = rows128 ? 128 : 256;
+    const int bm = gemm16_dma_rows(ta, tb, g.K);
+    const bool rows128 = bm == 128;
     g.tiles_m = (g.M + bm - 1) / bm;
     g.tiles_n = (g.N + kDT - 1) / kDT;
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
@@ -373,6 +373,8 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
 }
 
 }  // namespace
+
+int gemm16_dma_rows(bool ta, bool tb, int64_t K) { return ta || !tb || K <= 2048 ? 128 : 256; }
 
 int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (dtype == TT_BF16) return launch16_dma<__bf16>(ta, tb, g, st);
