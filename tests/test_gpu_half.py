@@ -138,15 +138,21 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
         (384, 256, 512, 1, 0),
         (256, 256, 2560, 1, 0),
         (200, 300, 512, 2, 0),
+        (256, 512, 256, 64, 0),
+        (264, 520, 256, 64, 0),
+        (256, 512, 2560, 128, 0),
     ],
 )
 def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     """Aligned leading dimensions (multiples of 8) take the 16-byte epilogue,
     odd ones (pad 3) and ragged column blocks the element-wise one. M, N >= 256
-    with aligned operands and K a multiple of 32, at least 256, run whole
-    tiles on the direct-load kernel and the ragged strips on the
-    register-staged one (520 x 264 x 1056, 200 x 300 x 512). Its tiles are
-    128 x 256, except 256 x 256 for NT beyond K = 2048 (256 x 256 x 2560)."""
+    with aligned operands, K a multiple of 32 of at least 256, at least 256
+    whole tiles and ragged strips of at most 1/16 of the outputs run whole
+    tiles on the direct-load kernel and the strips on the register-staged one
+    (64 x 264 x 520 x 256); 64 x 256 x 512 x 256 is whole tiles only. Its
+    tiles are 128 x 256, except 256 x 256 for NT beyond K = 2048
+    (128 x 256 x 512 x 2560). The smaller shapes run on the register-staged
+    kernel alone."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
 
@@ -156,6 +162,8 @@ def test_gemm16_d_aliases_c(hip, dt):
     """D may alias C exactly (header contract): D = alpha * AB + beta * D."""
     assert _gemm16_case(dt, False, True, 136, 264, 64, 2, 0.5, 2.0, True, alias=True, seed=3) <= BAR[dt]
     assert _gemm16_case(dt, True, False, 100, 90, 33, 1, 0.5, 2.0, True, pad=1, alias=True, seed=4) <= BAR[dt]
-    # the direct-load 256 x 256 kernel (whole tiles) and its ragged strips
     assert _gemm16_case(dt, False, False, 256, 512, 1024, 2, 0.5, 2.0, True, alias=True, seed=5) <= BAR[dt]
     assert _gemm16_case(dt, True, True, 520, 264, 1056, 1, 0.5, 2.0, True, alias=True, seed=6) <= BAR[dt]
+    # the direct-load kernel (whole tiles) and its ragged strips
+    assert _gemm16_case(dt, False, True, 256, 512, 256, 64, 0.5, 2.0, True, alias=True, seed=7) <= BAR[dt]
+    assert _gemm16_case(dt, True, False, 264, 520, 256, 64, 0.5, 2.0, True, alias=True, seed=8) <= BAR[dt]

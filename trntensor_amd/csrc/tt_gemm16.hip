@@ -327,8 +327,11 @@ int gemm16_staged(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // tiles of depth 32 run at 934-939 TFLOP/s against 840-862 for 128 x 128 x 64;
     // with A k-contiguous the 128 x 128 x 64 tile is the faster (857-872 against
     // 827-871). 128 x 256 x 32 and 128 x 128 x 32 tiles measured 802-922 and
-    // 710-868; 128 x 256 x 64 (one workgroup per CU) 500.
-    if (ta) return launch16<T, 256, 128, 32>(ta, tb, vec, g, st);
+    // 710-868; 128 x 256 x 64 (one workgroup per CU) 500. On smaller grids the
+    // 256 x 128 tile leaves CUs idle: 8 x 384 x 1024^2 41 against 282-288,
+    // 2048^3 252 against 394-399, 4096 x 256 x 4096 68 against 113-115.
+    if (ta && ((g.M + 255) / 256) * ((g.N + 127) / 128) * g.batch >= 512)
+        return launch16<T, 256, 128, 32>(ta, tb, vec, g, st);
     return launch16<T, 128, 128, 64>(ta, tb, vec, g, st);
 }
 
@@ -344,11 +347,21 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 398-403 against 400-401, TT 419 against 392-396; 64 x 512^3: 588-669
     // against 508-562).
     const int64_t kmin = 256;
+    // It also needs a full grid, and the ragged strips run as separate,
+    // serial launches: against the register-staged kernel alone it lost with
+    // 96-128 whole tiles (8 x 384 x 1024^2: 228-241 against 282-298 TFLOP/s;
+    // 2048^3: 359-387 against 394-411), tied at 192-256 (16 x 512 x 1024^2:
+    // 572-602 against 574-612) and won at 512 (4096^3 NN: 1104 against 850);
+    // with strips of a tenth of the outputs (2000 x 3000 x 320) it ran at
+    // 31-43 against 71-74.
     const int64_t bm = gemm16_dma_rows(ta, tb, g.K);
-    if (!vec || g.M < bm || g.N < 256 || g.K < kmin || g.K % 32 != 0) return gemm16_staged<T>(ta, tb, g, st);
+    const int64_t Mi = g.M & ~(bm - 1), Ni = g.N & ~(int64_t)255;
+    const int64_t tiles = (Mi / bm) * (Ni / 256) * g.batch;
+    const bool small_strips = (g.M - Mi) * g.N + Mi * (g.N - Ni) <= g.M * g.N / 16;
+    if (!vec || g.M < bm || g.N < 256 || g.K < kmin || g.K % 32 != 0 || tiles < 256 || !small_strips)
+        return gemm16_staged<T>(ta, tb, g, st);
     // Whole bm x 256 tiles by the direct-load kernel; the ragged row and
     // column strips (if any) by the register-staged kernel on sub-matrices.
-    const int64_t Mi = g.M & ~(bm - 1), Ni = g.N & ~(int64_t)255;
     const unsigned short* A = static_cast<const unsigned short*>(g.A);
     const unsigned short* B = static_cast<const unsigned short*>(g.B);
     const unsigned short* C = static_cast<const unsigned short*>(g.C);
