@@ -72,9 +72,10 @@ def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
     "ta,tb,M,N,K,batch",
     [
         (False, False, 64, 300, 70, 2),  # 64 x 128 tiles (M <= 64)
-        (True, False, 200, 150, 40, 3),  # 64 x 128 (fp64 batched, K <= 1024) / 128 x 128 (fp32)
+        (True, False, 200, 150, 40, 3),  # 64 x 128 (fp64 batched, K <= 1024; small grid)
         (False, True, 300, 50, 90, 1),  # 256 x 64 tiles (N <= 64)
-        (True, True, 257, 300, 129, 1),  # 128 x 128 tiles, ragged edges
+        (True, True, 257, 300, 129, 1),  # 64 x 128 tiles (small grid), ragged edges
+        (False, True, 2700, 2700, 40, 1),  # 128 x 128 tiles (484 of them), ragged edges
     ],
 )
 def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
