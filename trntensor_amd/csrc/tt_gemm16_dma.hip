@@ -27,8 +27,9 @@
 //     bytes) at kr * 2 ROWS, global piece p at position p ^ (2 (kr & 3)).
 // Direct load q (0..ROWS/16 - 1) of an operand fills bytes [1024 q, 1024 q +
 // 1024); wave w issues q = w, w + 4, ..., and lane l writes position l.
-// Workgroups whose tile crosses the matrix edge, and the K tail, stage the
-// same layout through registers with bounds checks (zero fill).
+// The host launches this kernel on whole tiles only (K a multiple of 32,
+// 16-byte aligned operands); ragged row and column strips run on the
+// register-staged kernel.
 #include <type_traits>
 
 #include "tt_gemm.hpp"
@@ -106,28 +107,6 @@ struct DStage {
             src(q, lane, r, k);
             const unsigned short* g = KC ? p + (row0 + r) * ld + k0 + k : p + (k0 + k) * ld + row0 + r;
             dma16(g, slot_off + 1024 * q);
-        }
-    }
-
-    // Edge or tail stage: the same layout through registers; elements outside
-    // rows x kdim are zero, and no address outside them is read.
-    __device__ __forceinline__ static void masked(const unsigned short* p, int64_t ld, int64_t row0, int64_t rows,
-                                                  int64_t k0, int64_t kdim, unsigned char* slot, int wave, int lane) {
-#pragma unroll 1
-        for (int i = 0; i < ROWS / 64; ++i) {
-            const int q = wave + 4 * i;
-            int r, k;
-            src(q, lane, r, k);
-            du16x8 v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int64_t gr = row0 + r + (KC ? 0 : e);
-                const int64_t gk = k0 + k + (KC ? e : 0);
-                const bool ok = gr < rows && gk < kdim;
-                const unsigned short x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
-                v[e] = ok ? x : (unsigned short)0;
-            }
-            *reinterpret_cast<du16x8*>(slot + 1024 * q + 16 * lane) = v;
         }
     }
 
