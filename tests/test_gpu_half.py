@@ -139,20 +139,23 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
         (256, 256, 2560, 1, 0),
         (200, 300, 512, 2, 0),
         (256, 512, 256, 64, 0),
-        (264, 520, 256, 64, 0),
+        (1032, 1024, 256, 16, 0),
+        (256, 512, 256, 16, 0),
+        (2056, 1024, 256, 1, 0),
         (256, 512, 2560, 128, 0),
     ],
 )
 def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     """Aligned leading dimensions (multiples of 8) take the 16-byte epilogue,
     odd ones (pad 3) and ragged column blocks the element-wise one. M, N >= 256
-    with aligned operands, K a multiple of 32 of at least 256, at least 256
-    whole tiles and ragged strips of at most 1/16 of the outputs run whole
+    with aligned operands, K a multiple of 32 of at least 256, at least 64
+    whole tiles and ragged strips of at most 1/64 of the outputs run whole
     tiles on the direct-load kernel and the strips on the register-staged one
-    (64 x 264 x 520 x 256); 64 x 256 x 512 x 256 is whole tiles only. Its
-    tiles are 128 x 256, except 256 x 256 for NT beyond K = 2048
-    (128 x 256 x 512 x 2560). The smaller shapes run on the register-staged
-    kernel alone."""
+    (16 x 1032 x 1024 x 256, 2056 x 1024 x 256). Its tiles are 128 x 256
+    (64 x 256 x 512 x 256, 16 x 1032 x 1024 x 256), 256 x 256 for NT beyond
+    K = 2048 (128 x 256 x 512 x 2560), and 128 x 128 when fewer than 256
+    tiles of 128 x 256 exist (16 x 256 x 512 x 256, 2056 x 1024 x 256). The
+    smaller shapes run on the register-staged kernel alone."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
 
@@ -166,4 +169,5 @@ def test_gemm16_d_aliases_c(hip, dt):
     assert _gemm16_case(dt, True, True, 520, 264, 1056, 1, 0.5, 2.0, True, alias=True, seed=6) <= BAR[dt]
     # the direct-load kernel (whole tiles) and its ragged strips
     assert _gemm16_case(dt, False, True, 256, 512, 256, 64, 0.5, 2.0, True, alias=True, seed=7) <= BAR[dt]
-    assert _gemm16_case(dt, True, False, 264, 520, 256, 64, 0.5, 2.0, True, alias=True, seed=8) <= BAR[dt]
+    assert _gemm16_case(dt, True, False, 1032, 1024, 256, 16, 0.5, 2.0, True, alias=True, seed=8) <= BAR[dt]
+    assert _gemm16_case(dt, True, True, 2056, 1024, 256, 1, 0.5, 2.0, True, alias=True, seed=9) <= BAR[dt]

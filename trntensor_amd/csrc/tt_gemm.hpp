@@ -35,10 +35,12 @@ int gemm_dd_dispatch(bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // 16-bit GEMM (dtype TT_BF16 / TT_F16) on the 16x16x32 MFMA; same arguments.
 int gemm16_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
 // Its direct-load variant: 16-byte aligned operands (A, B, lda, ldb and
-// batch strides multiples of 8 elements), whole tiles of gemm16_dma_rows
-// rows by 256 columns, K a multiple of 32.
+// batch strides multiples of 8 elements), whole tiles of gemm16_dma_tile,
+// K a multiple of 32. gemm16_dma_rows: the tile height for a layout and K.
 int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st);
 int gemm16_dma_rows(bool ta, bool tb, int64_t K);
+// Its tile (bm x bn) for an M x N x K problem of `batch` products.
+void gemm16_dma_tile(bool ta, bool tb, int64_t M, int64_t N, int64_t K, int64_t batch, int& bm, int& bn);
 // Dot epilogue; writes one double per workgroup to g.partial and returns the
 // number of workgroups in *nparts.
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);

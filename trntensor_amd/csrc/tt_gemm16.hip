@@ -353,14 +353,22 @@ int gemm16_typed(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 2048^3: 359-387 against 394-411), tied at 192-256 (16 x 512 x 1024^2:
     // 572-602 against 574-612) and won at 512 (4096^3 NN: 1104 against 850);
     // with strips of a tenth of the outputs (2000 x 3000 x 320) it ran at
-    // 31-43 against 71-74.
-    const int64_t bm = gemm16_dma_rows(ta, tb, g.K);
-    const int64_t Mi = g.M & ~(bm - 1), Ni = g.N & ~(int64_t)255;
-    const int64_t tiles = (Mi / bm) * (Ni / 256) * g.batch;
-    const bool small_strips = (g.M - Mi) * g.N + Mi * (g.N - Ni) <= g.M * g.N / 16;
-    if (!vec || g.M < bm || g.N < 256 || g.K < kmin || g.K % 32 != 0 || tiles < 256 || !small_strips)
+    // 31-43 against 71-74. Its 128 x 128 tile (three workgroups per CU) takes
+    // the grids too small for 128 x 256 and beats the register-staged kernel
+    // on the same grid from 64 tiles (2048^3: 512-544 against 397-406;
+    // 8 x 384 x 1024^2: 320-335 against 293-302; 4096 x 256 x 4096: 151-162
+    // against 113-117, NT 112 against 113); with strips of 5.8% of the
+    // outputs (2000 x 3000 x 320) it lost again, 42-48 against 71-75, so
+    // strips are limited to 1/64.
+    int bm_, bn_;
+    gemm16_dma_tile(ta, tb, g.M, g.N, g.K, g.batch, bm_, bn_);
+    const int64_t bm = bm_, bn = bn_;
+    const int64_t Mi = g.M & ~(bm - 1), Ni = g.N & ~(bn - 1);
+    const int64_t tiles = (Mi / bm) * (Ni / bn) * g.batch;
+    const bool small_strips = (g.M - Mi) * g.N + Mi * (g.N - Ni) <= g.M * g.N / 64;
+    if (!vec || g.M < bm || g.N < bn || g.K < kmin || g.K % 32 != 0 || tiles < 64 || !small_strips)
         return gemm16_staged<T>(ta, tb, g, st);
-    // Whole bm x 256 tiles by the direct-load kernel; the ragged row and
+    // Whole bm x bn tiles by the direct-load kernel; the ragged row and
     // column strips (if any) by the register-staged kernel on sub-matrices.
     const unsigned short* A = static_cast<const unsigned short*>(g.A);
     const unsigned short* B = static_cast<const unsigned short*>(g.B);

@@ -1,18 +1,19 @@
 // 16-bit GEMM, large-tile variant (dtype TT_BF16 / TT_F16 of tt_gemm when
 // M, N >= 256): the same arithmetic as gemm16_kernel (v_mfma_f32_16x16x32,
 // fp32 accumulators, alpha/beta in fp32, one rounding at the store) with
-//  - BM x 256 workgroup tiles, four wavefronts of (BM / 2) x 128;
-//    BM = 256: 8 x 8 MFMA blocks per wave, 256 fp32 accumulators per lane
+//  - BM x BN workgroup tiles, four wavefronts of (BM / 2) x (BN / 2);
+//    256 x 256: 8 x 8 MFMA blocks per wave, 256 fp32 accumulators per lane
 //    (AGPRs; this file is built without the VGPR-accumulator option the other
-//    kernels use), one workgroup per CU; BM = 128: 4 x 8 blocks, two
+//    kernels use), one workgroup per CU; 128 x 256: 4 x 8 blocks, two
 //    workgroups per CU, whose independent barriers let one workgroup's MFMAs
-//    run while the other waits,
+//    run while the other waits; 128 x 128 (small grids): 4 x 4 blocks, three
+//    workgroups per CU,
 //  - operands copied global -> LDS by the direct-load path
 //    (global_load_lds_dwordx4: no VGPR staging and no ds_write), 16 bytes per
 //    lane, one kilobyte of LDS per wavefront instruction,
 //  - an LDS ring of 32-deep stages, one barrier per stage: four slots with
-//    three stages in flight (BM = 256, 128 KB) or three slots with two in
-//    flight (BM = 128, 72 KB).
+//    three stages in flight (256 x 256, 128 KB) or three slots with two in
+//    flight (128 x 256, 72 KB; 128 x 128, 48 KB).
 // BM = 256: per stage a wave issues 64 MFMAs (1024 MFMA cycles) against 16 KB
 // of LDS reads; the four waves together read 64 KB and the direct loads write
 // 32 KB, 96 bytes per clock at the full MFMA rate, of the 256 the LDS serves
@@ -144,16 +145,18 @@ __device__ __forceinline__ unsigned short dfrom_f32(float x) {
     return __builtin_bit_cast(unsigned short, (T)x);
 }
 
-template <typename T, bool TA, bool TB, int BM>
-__global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(GemmArgs g) {
+template <typename T, bool TA, bool TB, int BM, int BN>
+__global__ __launch_bounds__(256, BN == 128 ? 3 : (BM == 128 ? 2 : 1)) void gemm16_dma_kernel(GemmArgs g) {
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
     typedef DStage<!TA, BM> SA;
-    typedef DStage<TB> SB;
+    typedef DStage<TB, BN> SB;
     constexpr int FM = BM / 32;                 // 16-row MFMA blocks per wave
+    constexpr int FN = BN / 32;                 // 16-column MFMA blocks per wave
+    constexpr int WN = BN / 2;                  // wave tile columns
     constexpr int NS = BM == 256 ? kSlots : 3;  // ring slots
     constexpr int AB = BM * kDK * 2;            // A bytes per stage
-    constexpr int SB_ = AB + kOpBytes;          // slot bytes
-    constexpr int DPW = BM / 64 + 4;            // direct loads per wave per stage
+    constexpr int SB_ = AB + BN * kDK * 2;      // slot bytes
+    constexpr int DPW = BM / 64 + BN / 64;      // direct loads per wave per stage
     __shared__ __attribute__((aligned(1024))) unsigned char lds[NS * SB_];
 
     const int64_t tiles = g.tiles_m * g.tiles_n;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
     const int64_t gsize = min(g.tiles_m - first_m, GROUP);
     const int64_t rem = t - grp * GROUP * g.tiles_n;
     const int64_t m0 = (first_m + rem % gsize) * BM;
-    const int64_t n0 = (rem / gsize) * kDT;
+    const int64_t n0 = (rem / gsize) * BN;
 
     const unsigned short* A = static_cast<const unsigned short*>(g.A) + bat * g.sA;
     const unsigned short* B = static_cast<const unsigned short*>(g.B) + bat * g.sB;
@@ -176,31 +179,31 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
     // offset (M0) in scalar registers.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm0 = (wave >> 1) * (BM / 2);
-    const int wn0 = (wave & 1) * 128;
+    const int wn0 = (wave & 1) * WN;
 
     // The host launches this kernel on whole tiles only (M, N multiples of
     // 256 within the launch, K a multiple of 32, 16-byte aligned operands).
     const int64_t nk = g.K / kDK;
     auto slot = [&](int64_t s) __attribute__((always_inline)) -> unsigned char* { return lds + ((int)s % NS) * SB_; };
 
-    df32x4 acc[FM][8];
+    df32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = df32x4{0, 0, 0, 0};
+        for (int j = 0; j < FN; ++j) acc[i][j] = df32x4{0, 0, 0, 0};
 
-    auto read = [&](du16x8 (&fa)[FM], du16x8 (&fb)[8], int64_t s) __attribute__((always_inline)) {
+    auto read = [&](du16x8 (&fa)[FM], du16x8 (&fb)[FN], int64_t s) __attribute__((always_inline)) {
         const unsigned char* sl = slot(s);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) fb[j] = SB::frag(sl + AB, wn0 + 16 * j, lane);
+        for (int j = 0; j < FN; ++j) fb[j] = SB::frag(sl + AB, wn0 + 16 * j, lane);
 #pragma unroll
         for (int i = 0; i < FM; ++i) fa[i] = SA::frag(sl, wm0 + 16 * i, lane);
     };
-    auto mfma = [&](du16x8 (&fa)[FM], du16x8 (&fb)[8]) __attribute__((always_inline)) {
+    auto mfma = [&](du16x8 (&fa)[FM], du16x8 (&fb)[FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[i][j] = mma16<T>(fa[i], fb[j], acc[i][j]);
+            for (int j = 0; j < FN; ++j) acc[i][j] = mma16<T>(fa[i], fb[j], acc[i][j]);
     };
     // Make stage s readable by every wave, with `ahead` direct-loaded stages
     // issued after it: this wave's direct loads of stage s are its oldest
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
         // Stages issued after stage kt: those below min(nk, kt + NS - 1).
         ready(min<int64_t>(nk, kt + NS - 1) - (kt + 1));
         if (kt + NS - 1 < nk) dma(kt + NS - 1);
-        du16x8 fa[FM], fb[8];
+        du16x8 fa[FM], fb[FN];
         read(fa, fb, kt);
         mfma(fa, fb);
         // Software pipeline for the scheduler: the B fragments and the first
@@ -245,13 +248,13 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
         // each A read right before its row, behind a full wait).
         constexpr int RA = TA ? 2 : 1;  // LDS read instructions per A fragment
         constexpr int RB = TB ? 1 : 2;  // per B fragment
-        __builtin_amdgcn_sched_group_barrier(0x100, 8 * RB + 2 * RA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, FN * RB + 2 * RA, 0);
 #pragma unroll
         for (int i = 0; i < FM - 2; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * FN, 0);
     }
     __syncthreads();
 
@@ -262,7 +265,8 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
     unsigned short* D = static_cast<unsigned short*>(g.D) + bat * g.sD;
     const float alpha = (float)g.alpha;
     const float beta = (float)g.beta;
-    constexpr int SP = 128 + 4;  // slab pitch in floats
+    constexpr int SP = WN + 4;  // slab pitch in floats
+    constexpr int CPR = WN / 8;  // 8-column chunks per slab row
     static_assert(4 * 16 * SP * sizeof(float) <= sizeof(lds), "epilogue slabs fit in the ring");
     float* slab = reinterpret_cast<float*>(lds) + wave * 16 * SP;
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -274,18 +278,18 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
         // slab exchange, whose barrier then covers their latency): D may
         // alias C, so the compiler cannot move a load of C past a store of D,
         // and chunk-by-chunk loads would each wait out a full memory latency.
-        du16x8 cc[4];
+        du16x8 cc[16 * CPR / 64];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < 16 * CPR / 64; ++h) {
             const int v = lane + 64 * h;
-            const int rr = v >> 4, cb = v & 15;
+            const int rr = v / CPR, cb = v % CPR;
             const int64_t row = m0 + wm0 + 16 * i + rr;
             const int64_t col = n0 + wn0 + 8 * cb;
             cc[h] = du16x8{0, 0, 0, 0, 0, 0, 0, 0};
             if (C && vout && row < g.M && col + 8 <= g.N) cc[h] = *reinterpret_cast<const du16x8*>(C + row * g.ldc + col);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float v = acc[i][j][r];
@@ -294,9 +298,9 @@ __global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void gemm16_dma_kernel(Gemm
             }
         __syncthreads();
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < 16 * CPR / 64; ++h) {
             const int v = lane + 64 * h;
-            const int rr = v >> 4, cb = v & 15;
+            const int rr = v / CPR, cb = v % CPR;
             const int64_t row = m0 + wm0 + 16 * i + rr;
             const int64_t col = n0 + wn0 + 8 * cb;
             const df32x4 lo = *reinterpret_cast<const df32x4*>(slab + rr * SP + 8 * cb);
@@ -336,24 +340,40 @@ int launch16_dma(bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     // 987-989 against 980-992, 4096^3 1013 against 1043; TT x 1024 846-850
     // against 747-754, x 2048 993-995 against 921-946, 4096^3 1088-1091
     // against 1070-1077.
-    const int bm = gemm16_dma_rows(ta, tb, g.K);
+    int bm, bn;
+    gemm16_dma_tile(ta, tb, g.M, g.N, g.K, g.batch, bm, bn);
     const bool rows128 = bm == 128;
     g.tiles_m = (g.M + bm - 1) / bm;
-    g.tiles_n = (g.N + kDT - 1) / kDT;
+    g.tiles_n = (g.N + bn - 1) / bn;
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const dim3 grid((unsigned)total), block(256);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false, 128>), grid, block, 0, st, g);
-    if (!ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128>), grid, block, 0, st, g);
-    if (!ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 256>), grid, block, 0, st, g);
-    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 128>), grid, block, 0, st, g);
-    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128>), grid, block, 0, st, g);
+    if (bn == 128) {
+        if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false, 128, 128>), grid, block, 0, st, g);
+        if (!ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128, 128>), grid, block, 0, st, g);
+        if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 128, 128>), grid, block, 0, st, g);
+        if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128, 128>), grid, block, 0, st, g);
+        return check_launch("tt_gemm (16-bit, direct loads)");
+    }
+    if (!ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, false, 128, 256>), grid, block, 0, st, g);
+    if (!ta && tb && rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 128, 256>), grid, block, 0, st, g);
+    if (!ta && tb && !rows128) hipLaunchKernelGGL((gemm16_dma_kernel<T, false, true, 256, 256>), grid, block, 0, st, g);
+    if (ta && !tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, false, 128, 256>), grid, block, 0, st, g);
+    if (ta && tb) hipLaunchKernelGGL((gemm16_dma_kernel<T, true, true, 128, 256>), grid, block, 0, st, g);
     return check_launch("tt_gemm (16-bit, direct loads)");
 }
 
 }  // namespace
 
 int gemm16_dma_rows(bool ta, bool tb, int64_t K) { return ta || !tb || K <= 2048 ? 128 : 256; }
+
+// Tile of the direct-load kernel: bm rows as above; 128 columns instead of 256
+// (three workgroups per CU) when fewer than 256 tiles of 128 x 256 would run.
+void gemm16_dma_tile(bool ta, bool tb, int64_t M, int64_t N, int64_t K, int64_t batch, int& bm, int& bn) {
+    bm = gemm16_dma_rows(ta, tb, K);
+    bn = 256;
+    if (bm == 128 && (M / 128) * (N / 256) * batch < 256) bn = 128;
+}
 
 int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st) {
     if (dtype == TT_BF16) return launch16_dma<__bf16>(ta, tb, g, st);
