@@ -76,8 +76,13 @@ struct Stage16 {
     }
 
     // FAST: interior stage, 16-byte aligned lines: unconditional vector loads.
-    // Otherwise element loads from clamped addresses, zero outside.
-    template <bool FAST>
+    // Otherwise (a tile crossing the matrix edge, the K tail, or unaligned
+    // lines) piece by piece: a piece wholly inside is one vector load (VEC:
+    // aligned lines), one wholly outside is zero without a load, and only a
+    // piece that straddles the edge is loaded element by element from clamped
+    // addresses. (Element loads for every piece made edge tiles, and so whole
+    // ragged launches, 4-7x slower than aligned ones of the same size.)
+    template <bool FAST, bool VEC>
     __device__ __forceinline__ void load(const unsigned short* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
                                          int64_t k0, int64_t kdim) {
         int line, off;
@@ -88,15 +93,26 @@ struct Stage16 {
             for (int c = 0; c < NP; ++c) reg[c] = *reinterpret_cast<const u16x8*>(src + 8 * c);
         } else {
 #pragma unroll
-            for (int c = 0; c < NP; ++c)
+            for (int c = 0; c < NP; ++c) {
+                // Piece start (gr, gk) and its extent along the contiguous direction.
+                const int64_t gr = row0 + (KC ? line : off + 8 * c);
+                const int64_t gk = k0 + (KC ? off + 8 * c : line);
+                const bool inside = KC ? (gr < rows && gk + 8 <= kdim) : (gk < kdim && gr + 8 <= rows);
+                const bool outside = gr >= rows || gk >= kdim;
+                if (VEC && inside) {
+                    reg[c] = *reinterpret_cast<const u16x8*>(KC ? p + gr * ld + gk : p + gk * ld + gr);
+                } else if (outside) {
+                    reg[c] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int64_t gr = row0 + (KC ? line : off + 8 * c + e);
-                    const int64_t gk = k0 + (KC ? off + 8 * c + e : line);
-                    const bool ok = gr < rows && gk < kdim;
-                    const unsigned short x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
-                    reg[c][e] = ok ? x : (unsigned short)0;
+                    for (int e = 0; e < 8; ++e) {
+                        const int64_t r = gr + (KC ? 0 : e), k = gk + (KC ? e : 0);
+                        const bool ok = r < rows && k < kdim;
+                        const unsigned short x = *(ok ? (KC ? p + r * ld + k : p + k * ld + r) : p);
+                        reg[c][e] = ok ? x : (unsigned short)0;
+                    }
                 }
+            }
         }
     }
 
@@ -175,8 +191,8 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
     const int64_t nfull = (VEC && m0 + BM <= g.M && n0 + BN <= g.N) ? g.K / BK : 0;
     auto load = [&](int64_t k0, auto fast) {
         constexpr bool F = decltype(fast)::value;
-        sa.template load<F>(A, g.lda, m0, g.M, k0, g.K);
-        sb.template load<F>(B, g.ldb, n0, g.N, k0, g.K);
+        sa.template load<F, VEC>(A, g.lda, m0, g.M, k0, g.K);
+        sb.template load<F, VEC>(B, g.ldb, n0, g.N, k0, g.K);
     };
     auto compute = [&](int buf) {
         const unsigned short* a = bufA(buf);
