@@ -64,9 +64,13 @@ struct Stage {
     __device__ __forceinline__ static constexpr int piece(int c) { return KC ? c * V : c * 16 * V; }
 
     // FAST (interior stage: tile inside the matrix, 16-byte aligned):
-    // unconditional vector loads. Otherwise element-wise loads from clamped
-    // addresses, zeroing what lies outside; no per-lane branches (which would
-    // serialise the prefetch behind waits).
+    // unconditional vector loads. Otherwise (edge tiles, the K tail, unaligned
+    // operands) piece by piece: a piece wholly inside is one vector load (VEC),
+    // one wholly outside is zero without a load, and only a piece straddling
+    // the edge is loaded element-wise from clamped addresses. Measured against
+    // element-wise loads for every piece (fp32, fp64 TFLOP/s): 2000 x 3000 x
+    // 2000 106.5 and 57.3 against 77.0 and 51.0; 4000^3 TN 123.4 and 58.4
+    // against 95.7 and 53.6; aligned shapes unchanged.
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
                                          int64_t k0, int64_t kdim) {
@@ -79,14 +83,25 @@ struct Stage {
         } else {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
+                const int64_t pr = row0 + r + (KC ? 0 : piece(c));
+                const int64_t pk = k0 + k + (KC ? piece(c) : 0);
+                const bool inside = KC ? (pr < rows && pk + V <= kdim) : (pk < kdim && pr + V <= rows);
+                const bool outside = pr >= rows || pk >= kdim;
+                if (VEC && inside) {
+                    reg[c] = *reinterpret_cast<const vec_t*>(KC ? p + pr * ld + pk : p + pk * ld + pr);
+                } else if (outside) {
 #pragma unroll
-                for (int e = 0; e < V; ++e) {
-                    const int off = piece(c) + e;
-                    const int64_t gr = row0 + r + (KC ? 0 : off);
-                    const int64_t gk = k0 + k + (KC ? off : 0);
-                    const bool ok = gr < rows && gk < kdim;
-                    const T x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
-                    reg[c][e] = ok ? x : T(0);
+                    for (int e = 0; e < V; ++e) reg[c][e] = T(0);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const int off = piece(c) + e;
+                        const int64_t gr = row0 + r + (KC ? 0 : off);
+                        const int64_t gk = k0 + k + (KC ? off : 0);
+                        const bool ok = gr < rows && gk < kdim;
+                        const T x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
+                        reg[c][e] = ok ? x : T(0);
+                    }
                 }
             }
         }
