@@ -52,14 +52,24 @@ struct Panel {
     vec_t reg;
 
     // FAST (interior stage: all 64 rows present, BK k in range, aligned):
-    // one unconditional vector load. Otherwise element-wise loads from clamped
-    // addresses, zeroing what lies outside; no per-lane branches.
+    // one unconditional vector load. Otherwise (a block with fewer than 64
+    // rows, the K tail, or unaligned rows) this thread's E values are one
+    // vector load when all lie inside (VEC), zero without a load when all lie
+    // outside, and element loads from clamped addresses only when they
+    // straddle the end of the row. Element loads throughout made every unit
+    // of a ragged block slow: nocc 64, nvir 300, naux 1200 took 8.99 ms (fp64)
+    // and 6.22 ms (fp32) against 8.38 and 4.54 ms this way.
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
         const int r = threadIdx.x >> 2;
         const int k = (threadIdx.x & 3) * E;
         if (FAST) {
             reg = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
+        } else if (VEC && r < rows && k0 + k + E <= naux) {
+            reg = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
+        } else if (r >= rows || k0 + k >= naux) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) reg[e] = T(0);
         } else {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
