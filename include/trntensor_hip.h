@@ -134,6 +134,23 @@ int tt_mp2_energy(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
                   int deterministic, void* stream);
 
 /*
+ * tt_mp2_energy without a workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. Same arguments,
+ * kernels and result as tt_mp2_energy, bitwise; the partials (deterministic
+ * != 0: nocc(nocc+1)/2 * nblk(nblk+1)/2 + 1 doubles, nblk = ceil(nvir/64))
+ * or the atomic accumulator (deterministic == 0: one double) live in a
+ * static device array of 2^21 doubles (16 MiB) that each device holds until
+ * the process ends. A deterministic problem needing more returns TT_INVALID.
+ * The call allocates nothing. Every call on one device shares that array,
+ * so calls that overlap on one device (different streams, or threads) race;
+ * calls ordered on one stream do not.
+ */
+int tt_mp2_energy_noalloc(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
+                          const void* B, const void* eps_occ, const void* eps_vir,
+                          void* energy_out, int deterministic, void* stream);
+
+/*
  * Workspace (device bytes) that tt_ao_to_mo_transform needs.
  */
 size_t tt_ao_to_mo_workspace_bytes(int dtype, int64_t nbasis, int64_t nocc, int64_t nvir, int64_t naux);

@@ -22,6 +22,7 @@
 // (trntensor/quantum.py:97-99): denominator ((e_i + e_j) - e_a) - e_b with a
 // the row index, term (T * (2T - T^T)) / denominator with IEEE division, in
 // the input dtype; the energy is accumulated in double.
+#include <mutex>
 #include <type_traits>
 
 #include "tt_common.hpp"
@@ -420,25 +421,97 @@ extern "C" size_t tt_mp2_energy_workspace_bytes(int dtype, int64_t nocc, int64_t
     return ((n * sizeof(double) + 255) / 256) * 256;
 }
 
+namespace tt {
+
+// Argument checks shared by both entry points (no HIP call).
+static int mp2_check(const char* what, int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B,
+                     const void* eps_occ, const void* eps_vir, const void* energy_out) {
+    if (nocc < 0 || nvir < 0 || naux < 0)
+        return set_error(TT_INVALID, "%s: negative extent (nocc=%lld nvir=%lld naux=%lld)", what, (long long)nocc,
+                         (long long)nvir, (long long)naux);
+    if (nocc > (1 << 20) || nvir > (1 << 24))
+        return set_error(TT_UNSUPPORTED, "%s: nocc=%lld nvir=%lld beyond the kernel's index range", what,
+                         (long long)nocc, (long long)nvir);
+    if (mp2_ntasks(nocc, nvir) > 0x7fffffffLL)
+        return set_error(TT_UNSUPPORTED, "%s: too many work units for one launch", what);
+    if (!energy_out || (nocc > 0 && nvir > 0 && (!B || !eps_occ || !eps_vir)))
+        return set_error(TT_INVALID, "%s: NULL pointer", what);
+    if (dtype != TT_F64 && dtype != TT_F32)
+        return set_error(TT_UNSUPPORTED, "%s: dtype %d (only TT_F32, TT_F64)", what, dtype);
+    return TT_OK;
+}
+
+static int mp2_dispatch(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eo,
+                        const void* ev, void* out, void* ws, int det, hipStream_t st) {
+    if (dtype == TT_F64) return mp2_typed<double>(nocc, nvir, naux, B, eo, ev, out, ws, det, st);
+    return mp2_typed<float>(nocc, nvir, naux, B, eo, ev, out, ws, det, st);
+}
+
+// Scratch of the allocation-free entry point: the per-workgroup partials
+// (deterministic mode) or the atomic accumulator (element 0). One copy per
+// device, resident until the process ends. Host code never passes this
+// name to a kernel: it is a host-side stand-in, and the device address comes
+// from hipGetSymbolAddress (mp2_scratch_ptr below).
+constexpr int64_t kMp2ScratchDoubles = int64_t(1) << 21;  // 16 MiB
+static __device__ __align__(256) double scratch[kMp2ScratchDoubles];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+static int mp2_scratch_ptr(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(TT_HIP_ERROR, "tt_mp2_energy_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(TT_UNSUPPORTED, "tt_mp2_energy_noalloc: device index %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(TT_HIP_ERROR, "tt_mp2_energy_noalloc: hipGetSymbolAddress(scratch): %s",
+                             hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TT_OK;
+}
+
+}  // namespace tt
+
 extern "C" int tt_mp2_energy(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eps_occ,
                              const void* eps_vir, void* energy_out, void* workspace, size_t workspace_bytes,
                              int deterministic, void* stream) {
     using namespace tt;
-    if (nocc < 0 || nvir < 0 || naux < 0)
-        return set_error(TT_INVALID, "tt_mp2_energy: negative extent (nocc=%lld nvir=%lld naux=%lld)",
-                         (long long)nocc, (long long)nvir, (long long)naux);
-    if (nocc > (1 << 20) || nvir > (1 << 24))
-        return set_error(TT_UNSUPPORTED, "tt_mp2_energy: nocc=%lld nvir=%lld beyond the kernel's index range",
-                         (long long)nocc, (long long)nvir);
-    if (mp2_ntasks(nocc, nvir) > 0x7fffffffLL)
-        return set_error(TT_UNSUPPORTED, "tt_mp2_energy: too many work units for one launch");
-    if (!energy_out || (nocc > 0 && nvir > 0 && (!B || !eps_occ || !eps_vir)))
-        return set_error(TT_INVALID, "tt_mp2_energy: NULL pointer");
+    int rc = mp2_check("tt_mp2_energy", dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out);
+    if (rc != TT_OK) return rc;
     const size_t need = tt_mp2_energy_workspace_bytes(dtype, nocc, nvir, naux);
     if (!workspace || workspace_bytes < need)
         return set_error(TT_INVALID, "tt_mp2_energy: workspace of %zu bytes, need %zu", workspace_bytes, need);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dtype == TT_F64) return mp2_typed<double>(nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic, st);
-    if (dtype == TT_F32) return mp2_typed<float>(nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic, st);
-    return set_error(TT_UNSUPPORTED, "tt_mp2_energy: dtype %d (only TT_F32, TT_F64)", dtype);
+    return mp2_dispatch(dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tt_mp2_energy_noalloc(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B,
+                                     const void* eps_occ, const void* eps_vir, void* energy_out, int deterministic,
+                                     void* stream) {
+    using namespace tt;
+    int rc = mp2_check("tt_mp2_energy_noalloc", dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out);
+    if (rc != TT_OK) return rc;
+    // Deterministic mode keeps one partial per work unit; the atomic mode
+    // needs only the accumulator.
+    const int64_t need = deterministic ? mp2_ntasks(nocc, nvir) + 1 : 1;
+    if (need > kMp2ScratchDoubles)
+        return set_error(TT_INVALID,
+                         "tt_mp2_energy_noalloc: nocc=%lld nvir=%lld needs %lld partials, the static scratch holds "
+                         "%lld (use tt_mp2_energy with a workspace, or deterministic=0)",
+                         (long long)nocc, (long long)nvir, (long long)need, (long long)kMp2ScratchDoubles);
+    void* ws = nullptr;
+    rc = mp2_scratch_ptr(&ws);
+    if (rc != TT_OK) return rc;
+    return mp2_dispatch(dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, ws, deterministic,
+                        static_cast<hipStream_t>(stream));
 }
