@@ -120,20 +120,49 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
     lhs, out_str = _parse_subscripts(subscripts)
     terms = lhs.split(",")
 
+    # The reference finishes with result.add(out, alpha=beta)
+    # (trntensor/einsum.py:101-102): torch's type promotion and broadcasting.
+    # When `out` promotes to the contraction's dtype and broadcasts to its
+    # shape, beta*out is fused into the last kernel's store; otherwise the
+    # contraction (with alpha) is rounded to its own dtype first and a
+    # second pass adds beta*out in the promoted dtype and broadcast shape.
     C = None
+    post = None
     if out_dev is not None:
         shape = _result_shape(terms, out_str, ops)
-        C = out_dev.to(cd).expand(shape).contiguous()
+        final_dtype = torch.promote_types(res_dtype, out_dev.dtype)
+        final_shape = list(torch.broadcast_shapes(tuple(shape), tuple(out_dev.shape)))
+        if final_dtype == res_dtype and final_shape == shape:
+            C = out_dev.to(cd).expand(shape).contiguous()
+        else:
+            dispatch.compute_dtype(final_dtype)  # raises for dtypes the kernels do not compute in
+            post = (final_dtype, final_shape)
 
+    kb, kc = (beta, C) if post is None else (0.0, None)
     if plan.strategy == "path":
-        res = _execute_path(terms, out_str, ops, plan.contraction_path, alpha, beta, C)
+        res = _execute_path(terms, out_str, ops, plan.contraction_path, alpha, kb, kc)
     else:
         res = engine.contract(
-            terms, out_str, ops, alpha, beta, C, prefer_gemm=plan.strategy in ("matmul", "bmm")
+            terms, out_str, ops, alpha, kb, kc, prefer_gemm=plan.strategy in ("matmul", "bmm")
         )
     if res.dtype != res_dtype:
         res = res.to(res_dtype)
+    if post is not None:
+        res = _add_out(res, out_dev, beta, *post)
     return res if res.device == orig else res.to(orig)
+
+
+def _add_out(res: torch.Tensor, out: torch.Tensor, beta: float, dtype: torch.dtype, shape: list[int]) -> torch.Tensor:
+    """res + beta * out in `dtype`, broadcast to `shape` (one strided pass on the
+    device; 16-bit results are computed in float32 and rounded once)."""
+    cd = dispatch.compute_dtype(dtype)
+    r = res.to(cd)
+    lead = len(shape) - r.dim()
+    strides = [0] * lead + [0 if n == 1 and m != 1 else s for n, m, s in zip(r.shape, shape[lead:], r.stride())]
+    C = out.to(cd).expand(shape).contiguous()
+    D = torch.empty(shape, dtype=cd, device=res.device)
+    engine.strided_contract([(n, s, 0) for n, s in zip(shape, strides)], [], r, None, D, 1.0, beta, C)
+    return D if cd == dtype else D.to(dtype)
 
 
 def _result_shape(terms, out_str, ops) -> list[int]:
