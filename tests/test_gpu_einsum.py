@@ -150,6 +150,21 @@ class TestAlphaBetaDtypePrecision:
         assert kahan.dtype == torch.float32
         assert abs(float(kahan) - float(ref)) <= abs(float(fast) - float(ref)) + 1e-3
 
+    @pytest.mark.parametrize("sub,shapes", [("ij,jk->ik", [(4096, 4096), (4096, 4096)]),
+                                            ("bij,bjk->bik", [(64, 512, 512), (64, 512, 512)])])
+    def test_kahan_config2_scale(self, hip, sub, shapes):
+        """precision="kahan" on config-2 float32 operands: float64 contraction on
+        the device, rounded once to float32, against the oracle's kahan branch
+        (float64 torch on the CPU, cast once)."""
+        g = torch.Generator().manual_seed(0)
+        A, B = (torch.randn(*s, generator=g, dtype=torch.float64).float() for s in shapes)
+        got = trntensor.einsum(sub, A.cuda(), B.cuda(), precision="kahan")
+        ref = cpu_ref.einsum(sub, A, B, precision="kahan")
+        assert got.dtype == ref.dtype == torch.float32
+        assert normwise(got, ref) <= 2e-7
+        fast = cpu_ref.einsum(sub, A, B)
+        print(f"kahan {sub}: normwise vs oracle {normwise(got, ref):.2e}; fp32 CPU path {normwise(fast, ref):.2e}")
+
     def test_dd_computes(self, hip):
         """The reference raises NotImplementedError for precision='dd'
         (tests/test_einsum.py:328-333); this build computes it (double-double
@@ -163,6 +178,77 @@ class TestAlphaBetaDtypePrecision:
         torch.manual_seed(0)
         A, B = torch.randn(8, 6), torch.randn(6, 10)
         assert torch.equal(trntensor.einsum("ij,jk->ik", A, B), trntensor.einsum("ij,jk->ik", A, B, precision="fast"))
+
+
+class TestOutPromotionBroadcast:
+    """`out` of another dtype or shape: the reference returns
+    result.add(out, alpha=beta) (trntensor/einsum.py:101-102), so the result
+    takes torch's promoted dtype and broadcast shape. Checked against the
+    oracle (the same add) for dtype, shape and value; the value bar is that
+    of the contraction's own dtype, whose rounding the reference keeps."""
+
+    @staticmethod
+    def check(sub, shapes, dt, out_shape, out_dt, alpha=1.5, beta=0.5, device="cuda", seed=11):
+        g = torch.Generator().manual_seed(seed)
+        ops = [torch.randn(*s, generator=g, dtype=torch.float64).to(dt) for s in shapes]
+        out = torch.randn(*out_shape, generator=g, dtype=torch.float64).to(out_dt)
+        ref = cpu_ref.einsum(sub, *ops, alpha=alpha, beta=beta, out=out)
+        got = trntensor.einsum(sub, *[o.to(device) for o in ops], alpha=alpha, beta=beta, out=out.to(device))
+        assert got.dtype == ref.dtype, (got.dtype, ref.dtype)
+        assert tuple(got.shape) == tuple(ref.shape), (tuple(got.shape), tuple(ref.shape))
+        assert got.device.type == torch.device(device).type
+        bar = {torch.float64: 1e-12, torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}[dt]
+        assert normwise(got.float() if got.dtype in (torch.bfloat16, torch.float16) else got, ref.to(got.dtype)) <= bar
+
+    def test_fp32_operands_fp64_out(self, hip):
+        self.check("ij,jk->ik", [(70, 50), (50, 90)], torch.float32, (70, 90), torch.float64)
+
+    def test_fp64_operands_fp32_out(self, hip):
+        # promotes to the contraction's dtype: fused epilogue, float64 result
+        self.check("ij,jk->ik", [(70, 50), (50, 90)], torch.float64, (70, 90), torch.float32)
+
+    def test_fp32_bmm_fp64_out_cpu_operands(self, hip):
+        self.check("bij,bjk->bik", [(3, 40, 30), (3, 30, 20)], torch.float32, (3, 40, 20), torch.float64, device="cpu")
+
+    def test_out_broadcasts_into_result(self, hip):
+        self.check("ij,jk->ik", [(33, 17), (17, 45)], torch.float64, (1, 45), torch.float64)
+        self.check("ij,jk->ik", [(33, 17), (17, 45)], torch.float32, (45,), torch.float32)
+
+    def test_out_larger_than_result(self, hip):
+        self.check("ij,jk->ik", [(33, 17), (17, 45)], torch.float64, (4, 33, 45), torch.float64)
+        self.check("ij,jk->ik", [(33, 17), (17, 45)], torch.float32, (2, 33, 1), torch.float64)
+
+    def test_scalar_result_vector_out(self, hip):
+        self.check("i,i->", [(300,), (300,)], torch.float64, (5,), torch.float64)
+        self.check("ij,jk,kl->", [(6, 7), (7, 8), (8, 9)], torch.float32, (3, 1), torch.float64)
+
+    def test_path_fp32_operands_fp64_out(self, hip):
+        self.check("ij,jk,kl->il", [(20, 30), (30, 40), (40, 10)], torch.float32, (20, 10), torch.float64)
+
+    def test_bf16_operands_fp32_out(self, hip):
+        self.check("ij,jk->ik", [(64, 64), (64, 96)], torch.bfloat16, (64, 96), torch.float32, alpha=1.0)
+
+    def test_kahan_fp32_with_fp64_out(self, hip):
+        g = torch.Generator().manual_seed(12)
+        A, B = (torch.randn(*s, generator=g) for s in [(30, 40), (40, 20)])
+        out = torch.randn(30, 20, generator=g, dtype=torch.float64)
+        ref = cpu_ref.einsum("ij,jk->ik", A, B, alpha=2.0, beta=0.25, out=out, precision="kahan")
+        got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), alpha=2.0, beta=0.25, out=out.cuda(), precision="kahan")
+        assert got.dtype == ref.dtype == torch.float64
+        assert normwise(got, ref) <= 1e-7
+
+    def test_unbroadcastable_out_raises(self, hip):
+        A, B = torch.randn(4, 3), torch.randn(3, 5)
+        with pytest.raises(RuntimeError):
+            trntensor.einsum("ij,jk->ik", A, B, beta=1.0, out=torch.randn(4, 4))
+        with pytest.raises(RuntimeError):
+            cpu_ref.einsum("ij,jk->ik", A, B, beta=1.0, out=torch.randn(4, 4))
+
+    def test_out_not_written(self, hip):
+        out = torch.randn(2, 8, 6, dtype=torch.float64, device="cuda")
+        keep = out.clone()
+        trntensor.einsum("ij,jk->ik", torch.randn(8, 5, device="cuda"), torch.randn(5, 6, device="cuda"), beta=2.0, out=out)
+        assert torch.equal(out, keep)
 
 
 class TestBackendOnDevice:
@@ -264,7 +350,15 @@ class TestConfig5:
         ijP = torch.einsum("ibP,jb->ijP", ibP, B)
         ref = torch.einsum("ijP,ijP->", ijP, V)
         scale = torch.einsum("ijP,ijP->", torch.einsum("ibP,jb->ijP", torch.einsum("ia,abP->ibP", A.abs(), W.abs()), B.abs()), V.abs())
-        assert abs(float(got) - float(ref)) / float(scale) <= 1e-14
+        kappa = float(scale) / abs(float(ref))
+        err = abs(float(got) - float(ref))
+        print(f"config 5: E={float(got):.17g} ref={float(ref):.17g} kappa={kappa:.3e} "
+              f"rel={err / abs(float(ref)):.3e} cond-aware={err / float(scale):.3e}")
+        # Both bars of the north star: relative 1e-12, and 1e-14 against the
+        # same contraction over absolute values (kappa is about 1.1e6 here;
+        # float64 orderings of the CPU oracle agree to 1.4e-13 relative).
+        assert err / abs(float(ref)) <= 1e-12
+        assert err / float(scale) <= 1e-14
         assert got.shape == () and got.dtype == torch.float64
 
 

@@ -171,6 +171,69 @@ def test_dtype_and_precision_semantics():
         cpu_ref.einsum("ij,jk->ik", A, B, precision="dd")
 
 
+KAHAN_CASES = [
+    ("ij,jk->ik", [(40, 300), (300, 30)]),
+    ("bij,bjk->bik", [(3, 20, 200), (3, 200, 10)]),
+    ("mi,mnP->inP", [(30, 4), (30, 30, 12)]),
+    ("ij,jk,kl->il", [(10, 200), (200, 50), (50, 7)]),
+    ("i,i->", [(5000,), (5000,)]),
+]
+
+
+@pytest.mark.parametrize("sub,shapes", KAHAN_CASES)
+def test_kahan_branch_is_float64_rounded_once(sub, shapes):
+    """precision="kahan" (trntensor/einsum.py:108-111): the float64 contraction
+    of the float32 operands, cast once. Pinned against numpy's float64 einsum
+    cast once to float32: every element within one float32 rounding (the two
+    float64 sums differ only in order, which can move a value across a float32
+    rounding boundary). Data with large and small magnitudes, so that float32
+    accumulation (the planted mistake) misses the bar."""
+    g = torch.Generator().manual_seed(len(sub))
+    ops = []
+    for k, s in enumerate(shapes):
+        x = torch.randn(*s, generator=g, dtype=torch.float64)
+        if k == 0:
+            x = x * torch.where(torch.rand(*s, generator=g) < 0.1, 1e4, 1e-2)
+        ops.append(x.float())
+    got = cpu_ref.einsum(sub, *ops, precision="kahan")
+    assert got.dtype == torch.float32
+    want = np.einsum(sub, *[o.double().numpy() for o in ops]).astype(np.float32)
+    ulp = np.spacing(np.abs(want)).astype(np.float64)
+    diff = np.abs(got.numpy().astype(np.float64) - want.astype(np.float64))
+    assert np.all(diff <= ulp), float((diff / np.maximum(ulp, 1e-45)).max())
+    fast = cpu_ref.einsum(sub, *ops).numpy().astype(np.float64)
+    assert np.any(np.abs(fast - want.astype(np.float64)) > ulp), "data must tell fp32 accumulation apart"
+
+
+@pytest.mark.parametrize(
+    "dt,out_dt,out_shape,want_dt,want_shape",
+    [
+        (torch.float32, torch.float64, (6, 5), torch.float64, (6, 5)),
+        (torch.float64, torch.float32, (6, 5), torch.float64, (6, 5)),
+        (torch.float32, torch.float32, (5,), torch.float32, (6, 5)),
+        (torch.float64, torch.float64, (3, 6, 5), torch.float64, (3, 6, 5)),
+        (torch.float32, torch.float64, (2, 6, 1), torch.float64, (2, 6, 5)),
+        (torch.bfloat16, torch.float32, (6, 5), torch.float32, (6, 5)),
+        (torch.float32, torch.int64, (6, 5), torch.float32, (6, 5)),
+    ],
+)
+def test_out_promotion_and_broadcast(dt, out_dt, out_shape, want_dt, want_shape):
+    """trntensor/einsum.py:99-102: alpha scales the result in its own dtype, then
+    result.add(out, alpha=beta) promotes and broadcasts. Pinned by dtype and
+    shape tables (numpy's float promotion agrees) and a float64 closed form."""
+    g = torch.Generator().manual_seed(5)
+    A, B = (torch.randn(*s, generator=g, dtype=torch.float64).to(dt) for s in [(6, 4), (4, 5)])
+    out = (torch.randn(*out_shape, generator=g, dtype=torch.float64) * 10).to(out_dt)
+    got = cpu_ref.einsum("ij,jk->ik", A, B, alpha=1.5, beta=0.5, out=out)
+    assert got.dtype == want_dt and tuple(got.shape) == want_shape
+    if dt != torch.bfloat16 and out_dt != torch.int64:
+        np_dt = np.result_type(torch.empty(0, dtype=dt).numpy().dtype, torch.empty(0, dtype=out_dt).numpy().dtype)
+        assert np_dt == torch.empty(0, dtype=want_dt).numpy().dtype
+    want = 1.5 * (A.double() @ B.double()) + 0.5 * out.double()
+    bar = 1e-2 if dt == torch.bfloat16 else (1e-6 if torch.float32 in (dt, want_dt) else 1e-13)
+    assert (got.double() - want).abs().max() <= bar * want.abs().max()
+
+
 def test_path_step_naming():
     """trntensor/einsum.py:171-185 on the config-5 expression: 'iajb' then 'abij'."""
     terms = ["ia", "jb", "abP", "ijP"]
