@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c5,f1,a5)")
+    ap.add_argument("--only", default="", help="comma list of extra configs (c1,c2,c3,c4f32,c4naux,c5,f1,a5)")
     ap.add_argument("--skip-headline", action="store_true", help="run only the extra configs")
     ap.add_argument(
         "--calibrate-copy",
@@ -233,11 +233,13 @@ def main():
         return
     if args.skip_headline:
         extra = {}
-        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1", "a5"}
+        want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c4naux", "c5", "f1", "a5"}
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
         if "c4f32" in want:
             extra["c4_mp2_fp32"] = bench_c4_f32(torch, tt, dev, args)
+        if "c4naux" in want:
+            extra["c4_mp2_naux_sweep"] = bench_c4_naux(torch, tt, dev, args)
         if "c2" in want:
             extra["c2"] = bench_c2(torch, tt, dev, args)
         if "c1" in want:
@@ -301,13 +303,15 @@ def main():
     line["roofline"]["frac_measured_peak"] = round(achieved / 1e12 / peaks["mfma_f64_TFLOPs"], 4)
 
     extra = {}
-    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c5", "f1", "a5"}
+    want = set(filter(None, args.only.split(","))) or {"c1", "c2", "c3", "c4f32", "c4naux", "c5", "f1", "a5"}
     if not args.no_extra:
         if "c3" in want:
             extra["c3_ao_to_mo_half_fp64"] = bench_c3(torch, tt, dev, args)
             line["ao_to_mo_GBps"] = extra["c3_ao_to_mo_half_fp64"]["GB/s"]
         if "c4f32" in want:
             extra["c4_mp2_fp32"] = bench_c4_f32(torch, tt, dev, args)
+        if "c4naux" in want:
+            extra["c4_mp2_naux_sweep"] = bench_c4_naux(torch, tt, dev, args)
         if "c2" in want:
             extra["c2"] = bench_c2(torch, tt, dev, args)
         if "c1" in want:
@@ -445,6 +449,24 @@ def bench_c4_f32(torch, tt, dev, args):
         "GFLOP/s": round(flop / (wall * 1e-3) / 1e9, 1),
         "frac_mfma_f32": round(flop / (ev_ms * 1e-3) / PEAK["f32"], 4),
     }
+
+
+def bench_c4_naux(torch, tt, dev, args):
+    """Config 4 with auxiliary sizes whose rows are not 16-byte aligned
+    (real auxiliary basis sizes are arbitrary): the kernel narrows its global
+    loads to what naux keeps aligned (fp32: 8 bytes for even naux, 4 for odd;
+    fp64: 8 for odd) and keeps the branch-free interior loop."""
+    out = {}
+    for dt, key, peak in ((torch.float64, "f64", PEAK["f64"]), (torch.float32, "f32", PEAK["f32"])):
+        for naux in (1200, 1190, 1199, 1201):
+            print(f"bench: c4 naux {naux} {key}", file=sys.stderr, flush=True)
+            B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, dt, naux=naux))
+            _, ms = timed_steady(torch, lambda: tt.mp2_energy(B, eo, ev), max(5, args.steps))
+            flop = 2080 * 2 * 320**2 * naux
+            out[f"{key}_naux{naux}"] = {"ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+                                        "frac_mfma": round(flop / (ms * 1e-3) / peak, 4)}
+            del B, eo, ev
+    return out
 
 
 def bench_c2(torch, tt, dev, args):

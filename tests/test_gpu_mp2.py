@@ -59,6 +59,62 @@ def test_mp2_fp32_matches_oracle(hip, shape):
     assert rel(got, ref) <= 1e-5
 
 
+# naux with rows not 16-byte aligned: fp32 even (8-byte loads), odd (4-byte
+# loads); fp64 odd (8-byte loads). Full and ragged virtual blocks.
+UNALIGNED = [
+    (6, 130, 1190),
+    (4, 70, 1199),
+    (5, 64, 1201),
+    (3, 100, 102),
+    (2, 64, 6),
+    (3, 65, 10),
+    (4, 128, 35),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("shape", UNALIGNED)
+def test_mp2_unaligned_naux_matches_oracle(hip, shape, dtype):
+    B, eo, ev = inputs(*shape, dtype=dtype, seed=sum(shape) + 7)
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert got.dtype == dtype
+    assert rel(got, ref) <= (1e-10 if dtype == torch.float64 else 1e-5), (float(got), float(ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_mp2_misaligned_base_pointer(hip, dtype):
+    """B contiguous but starting one element past a 16-byte boundary (a view
+    into a larger buffer): the loads narrow to the base's alignment. The
+    energy equals the aligned copy's bitwise (same values, same order)."""
+    nocc, nvir, naux = 5, 70, 64
+    B, eo, ev = inputs(nocc, nvir, naux, dtype=dtype, seed=31)
+    buf = torch.zeros(B.numel() + 1, dtype=dtype, device="cuda")
+    buf[1:] = B.reshape(-1).cuda()
+    Bv = buf[1:].view(nocc, nvir, naux)
+    assert Bv.is_contiguous() and Bv.data_ptr() % 16 != 0
+    got = tt.mp2_energy(Bv, eo.cuda(), ev.cuda())
+    aligned = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert float(got) == float(aligned)
+    assert rel(got, cpu_ref.mp2_energy(B, eo, ev)) <= (1e-10 if dtype == torch.float64 else 1e-5)
+
+
+@pytest.mark.parametrize("b_dt,e_dt", [(torch.float32, torch.float64), (torch.float64, torch.float32)])
+def test_mp2_mixed_dtypes_promote(hip, b_dt, e_dt):
+    """The reference loop (trntensor/quantum.py:94-99) returns torch's promoted
+    dtype of B and the orbital energies. The product computes in that dtype;
+    the reference keeps the lower precision's rounding in T (float32 B) or in
+    the denominators (float32 energies), so the bar is float32's."""
+    B, eo, ev = inputs(6, 70, 48, seed=17)
+    B, eo, ev = B.to(b_dt), eo.to(e_dt), ev.to(e_dt)
+    ref = cpu_ref.mp2_energy(B, eo, ev)
+    got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
+    assert ref.dtype == got.dtype == torch.float64
+    assert rel(got, ref) <= 1e-5, (float(got), float(ref))
+    exact = tt.mp2_energy(B.double().cuda(), eo.double().cuda(), ev.double().cuda())
+    assert float(got) == float(exact)
+
+
 def test_mp2_cpu_tensors_round_trip(hip):
     """CPU operands are staged through the device; the result comes back on the CPU."""
     B, eo, ev = inputs(4, 40, 24, seed=9)

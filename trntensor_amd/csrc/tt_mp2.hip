@@ -42,42 +42,63 @@ constexpr int kMp2StageK = TT_MP2_STAGE_K;  // k per LDS stage
 // one row's BK contiguous values. MFMA step s of a stage gives lane group
 // g = lane / 16 the k index E g + s, so a lane's E values per stage are
 // adjacent in LDS and one vector read feeds E MFMAs.
-template <typename T, int BK, bool VEC>
+//
+// AW is the global access width in elements: each thread's E values are
+// E / AW loads of AW consecutive elements. The launcher picks the widest AW
+// (16, 8 or 4 bytes) that every row start (a multiple of naux from B's base)
+// keeps naturally aligned, so rows of any naux take the branch-free
+// interior loop; only the access width narrows.
+template <typename T, int BK, int AW>
 struct Panel {
     static constexpr int E = BK / 4;  // elements per thread, = MFMA steps per stage
+    static constexpr int NP = E / AW;  // global loads per thread per stage
     static constexpr int PITCH = BK + 16 / sizeof(T);
     static constexpr int ELEMS = kMp2Tile * PITCH;
     static_assert(BK == 8 || BK == 16, "stage depth");
+    static_assert(AW >= 1 && E % AW == 0 && AW * sizeof(T) <= 16, "access width");
     typedef typename VecN<T, E>::type vec_t;
+    typedef typename VecN<T, AW>::type piece_t;
 
     vec_t reg;
 
-    // FAST (interior stage: all 64 rows present, BK k in range, aligned):
-    // one unconditional vector load. Otherwise (a block with fewer than 64
-    // rows, the K tail, or unaligned rows) this thread's E values are one
-    // vector load when all lie inside (VEC), zero without a load when all lie
-    // outside, and element loads from clamped addresses only when they
-    // straddle the end of the row. Element loads throughout made every unit
-    // of a ragged block slow: nocc 64, nvir 300, naux 1200 took 8.99 ms (fp64)
-    // and 6.22 ms (fp32) against 8.38 and 4.54 ms this way.
+    __device__ __forceinline__ void put(int c, piece_t x) {
+#pragma unroll
+        for (int e = 0; e < AW; ++e) reg[c * AW + e] = x[e];
+    }
+
+    // FAST (interior stage: all 64 rows present, BK k in range): NP
+    // unconditional loads. Otherwise (a block with fewer than 64 rows, or
+    // the K tail) each AW-piece is one load when it lies inside, zero
+    // without a load when it lies outside, and element loads from clamped
+    // addresses only when it straddles the end of the row. Element loads
+    // throughout made every unit of a ragged block slow: nocc 64, nvir 300,
+    // naux 1200 took 8.99 ms (fp64) and 6.22 ms (fp32) against 8.38 and
+    // 4.54 ms this way.
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
         const int r = threadIdx.x >> 2;
         const int k = (threadIdx.x & 3) * E;
+        const T* row = base + (int64_t)r * naux;
         if (FAST) {
-            reg = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
-        } else if (VEC && r < rows && k0 + k + E <= naux) {
-            reg = *reinterpret_cast<const vec_t*>(base + (int64_t)r * naux + k0 + k);
-        } else if (r >= rows || k0 + k >= naux) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) reg[e] = T(0);
-        } else {
+            for (int c = 0; c < NP; ++c) put(c, *reinterpret_cast<const piece_t*>(row + k0 + k + c * AW));
+            return;
+        }
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int64_t gk = k0 + k + e;
-                const bool ok = r < rows && gk < naux;
-                const T x = *(ok ? base + (int64_t)r * naux + gk : base);
-                reg[e] = ok ? x : T(0);
+        for (int c = 0; c < NP; ++c) {
+            const int64_t gk = k0 + k + c * AW;
+            if (r < rows && gk + AW <= naux) {
+                put(c, *reinterpret_cast<const piece_t*>(row + gk));
+            } else if (r >= rows || gk >= naux) {
+#pragma unroll
+                for (int e = 0; e < AW; ++e) reg[c * AW + e] = T(0);
+            } else {
+#pragma unroll
+                for (int e = 0; e < AW; ++e) {
+                    const bool ok = gk + e < naux;
+                    const T x = *(ok ? row + gk + e : row);
+                    reg[c * AW + e] = ok ? x : T(0);
+                }
             }
         }
     }
@@ -117,14 +138,14 @@ __device__ __forceinline__ void tri_decode(int64_t idx, int n, int& x, int& y) {
 
 // K loop of one work unit: X = P0 Q0^T and, if NEED_Y, Y = P2 Q3^T, BK k per
 // stage. Stages whose successor is interior run in the first loop with
-// unconditional vector prefetch; the rest (edge rows, the K remainder, the
-// last stage) run in the second loop.
-template <typename T, int BK, bool VEC, bool NEED_Y>
+// unconditional prefetch; the rest (edge rows, the K remainder, the last
+// stage) run in the second loop.
+template <typename T, int BK, int AW, bool NEED_Y>
 __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* base1,
                                           const T* base2, const T* base3, int rows_p, int rows_q, int64_t naux,
                                           typename Mfma<T>::acc_t (&X)[2][2], typename Mfma<T>::acc_t (&Y)[2][2]) {
     typedef Mfma<T> MF;
-    typedef Panel<T, BK, VEC> PN;
+    typedef Panel<T, BK, AW> PN;
     constexpr int KS = PN::E;
     // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS.
     auto lds = [&](int b, int k) -> T* { return lds_base + (4 * b + k) * PN::ELEMS; };
@@ -134,7 +155,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     const int wc = (wave & 1) * 32;
     const int64_t nk = (naux + BK - 1) / BK;
     // Stages 0 .. nfull-1 are interior (all rows present, all BK k in range).
-    const int64_t nfull = (VEC && rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
+    const int64_t nfull = (rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
 
     PN s0, s1, s2, s3;
     auto load = [&](int64_t k0, auto fast) {
@@ -229,11 +250,11 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     }
 }
 
-template <typename T, int BK, bool VEC>
+template <typename T, int BK, int AW>
 __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
-    typedef Panel<T, BK, VEC> PN;
+    typedef Panel<T, BK, AW> PN;
 
     __shared__ __attribute__((aligned(16))) T lds[1][4][PN::ELEMS];
     __shared__ double red[4];
@@ -272,9 +293,9 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
         }
 
     if (ymode == 0)
-        mp2_kloop<T, BK, VEC, true>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
+        mp2_kloop<T, BK, AW, true>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
     else
-        mp2_kloop<T, BK, VEC, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
+        mp2_kloop<T, BK, AW, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
 
     const int lg = lane >> 4;
     if (ymode == 2) {
@@ -370,6 +391,15 @@ __global__ void zero_double_kernel(double* p) {
     if (threadIdx.x == 0) p[0] = 0.0;
 }
 
+// Largest of 16 / sizeof(T), ..., 2, 1 elements such that B's base and every
+// row start (multiples of naux elements from it) are aligned to that many
+// elements' bytes.
+static int mp2_access_width(size_t elem, int64_t naux, const void* B) {
+    int aw = (int)(16 / elem);
+    while (aw > 1 && ((naux % aw) != 0 || (reinterpret_cast<uintptr_t>(B) % (aw * elem)) != 0)) aw >>= 1;
+    return aw;
+}
+
 static int64_t mp2_ntasks(int64_t nocc, int64_t nvir) {
     const int64_t nblk = (nvir + kMp2Tile - 1) / kMp2Tile;
     return (nblk * (nblk + 1) / 2) * (nocc * (nocc + 1) / 2);
@@ -397,14 +427,18 @@ static int mp2_typed(int64_t nocc, int64_t nvir, int64_t naux, const void* B, co
         g.accum = w;
         hipLaunchKernelGGL(zero_double_kernel, dim3(1), dim3(64), 0, st, w);
     }
-    constexpr int V = Vec16<T>::n;
     constexpr int BK = kMp2StageK;
-    const bool vec = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && (naux % V == 0);
+    // Widest access (elements) that keeps every row start naturally aligned.
+    const int aw = mp2_access_width(sizeof(T), naux, B);
     if (g.ntasks > 0) {
-        if (vec)
-            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, true>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+        const dim3 grid((unsigned)g.ntasks), block(kMp2Threads);
+        constexpr int V = 16 / sizeof(T);
+        if (aw == V)
+            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, V>), grid, block, 0, st, g);
+        else if (aw == 2)
+            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, 2>), grid, block, 0, st, g);
         else
-            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, false>), dim3((unsigned)g.ntasks), dim3(kMp2Threads), 0, st, g);
+            hipLaunchKernelGGL((mp2_energy_kernel<T, BK, 1>), grid, block, 0, st, g);
     }
     hipLaunchKernelGGL(mp2_finalize_kernel<T>, dim3(1), dim3(256), 0, st, (const double*)w,
                        det ? g.ntasks : (int64_t)1, static_cast<T*>(out));

@@ -189,12 +189,18 @@ def _binary(sub: str, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
 def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
     """Fused DF-MP2 energy on tt_mp2_energy (reference _nki_mp2_energy, dispatch.py:240-283).
 
-    Returns a 0-D tensor of B's dtype on B's device.
+    Returns a 0-D tensor on B's device in the dtype the reference's loop
+    returns: torch's promotion of B's and the orbital energies' dtypes
+    (trntensor/quantum.py:94-99). Mixed dtypes are computed in that promoted
+    dtype; the reference forms T in B's dtype and the denominators in the
+    orbital energies' dtype, so its result carries the lower precision's
+    rounding (the tests bound the difference at the float32 bar).
     """
     require_hip()
     lib = _lib.load()
     (b, eo, ev), orig = place(B, eps_occ, eps_vir)
-    cd = compute_dtype(b.dtype)
+    res_dtype = torch.promote_types(torch.promote_types(b.dtype, eo.dtype), ev.dtype)
+    cd = compute_dtype(res_dtype)
     b = b.to(cd).contiguous()
     eo = eo.to(cd).contiguous()
     ev = ev.to(cd).contiguous()
@@ -218,7 +224,7 @@ def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
         engine._stream_ptr(b.device),
     )
     _lib.check(st, "tt_mp2_energy")
-    return e.to(B.dtype).to(orig)
+    return e.to(res_dtype).to(orig)
 
 
 def _hip_ao_to_mo_transform(eri: torch.Tensor, C_occ: torch.Tensor, C_vir: torch.Tensor) -> torch.Tensor:
