@@ -26,24 +26,25 @@ constexpr int kBK = 16;
 constexpr int kThreads = 256;
 
 
-// One operand's ROWS x 16 stage: global -> registers -> LDS, plus fragment reads.
+// One operand's ROWS x BK stage: global -> registers -> LDS, plus fragment reads.
 // KC: element (row, k) at p[row * ld + k]; otherwise at p[k * ld + row].
-// Each thread stages E = ROWS / 16 elements as NC 16-byte pieces from one
-// address at immediate offsets:
-//   KC: row t / (16 / E), one contiguous chunk from k = (t % (16 / E)) E;
-//   RC: k-row t / 16, pieces (t % 16) + 16 c, so every instruction covers 256
+// Each thread stages E = ROWS * BK / 256 elements as NC 16-byte pieces:
+//   KC: row t / (BK / E), one contiguous chunk from k = (t % (BK / E)) E;
+//   RC: 16 threads per k-row, k-rows t / 16 + 16 j; within a k-row a
+//       thread's pieces are (t % 16) + 16 c, so every instruction covers 256
 //       contiguous bytes of the k-row (coalesced loads, conflict-free stores).
 // RC k-rows are padded by 4 elements: the four lane groups of a fragment read
 // (k-rows 4 g + s) then land on disjoint LDS banks.
-template <typename T, int ROWS, bool KC, bool VEC>
+template <typename T, int ROWS, bool KC, bool VEC, int BK>
 struct Stage {
     static constexpr int V = Vec16<T>::n;
-    static constexpr int E = ROWS * kBK / kThreads;
+    static constexpr int E = ROWS * BK / kThreads;
     static constexpr int NC = E / V;  // 16-byte pieces per thread
+    static constexpr int NCR = KC ? NC : ROWS / (16 * V);  // RC: pieces per k-row and thread
     static constexpr int PAD = 16 / sizeof(T);
-    static constexpr int PITCH = KC ? (kBK + PAD) : (ROWS + 4);
-    static constexpr int ELEMS = KC ? ROWS * PITCH : kBK * PITCH;
-    static_assert(E % V == 0 && E <= kBK * (KC ? 1 : ROWS), "stage split");
+    static constexpr int PITCH = KC ? (BK + PAD) : (ROWS + 4);
+    static constexpr int ELEMS = KC ? ROWS * PITCH : BK * PITCH;
+    static_assert(BK % 16 == 0 && E % V == 0 && (KC ? BK % E == 0 : (NC % NCR == 0 && NCR >= 1)), "stage split");
     typedef typename Vec16<T>::type vec_t;
 
     vec_t reg[NC];
@@ -51,17 +52,16 @@ struct Stage {
     __device__ __forceinline__ static void place(int& row, int& k) {
         const int t = threadIdx.x;
         if (KC) {
-            row = t / (kBK / E);
-            k = (t % (kBK / E)) * E;
+            row = t / (BK / E);
+            k = (t % (BK / E)) * E;
         } else {
-            // 16 threads per k-row; a thread's NC pieces sit 16 pieces apart so
-            // each instruction covers 256 contiguous bytes of the row.
             k = t / 16;
             row = (t % 16) * V;
         }
     }
-    // Element offset (along the contiguous direction) of piece c relative to piece 0.
-    __device__ __forceinline__ static constexpr int piece(int c) { return KC ? c * V : c * 16 * V; }
+    // Offsets of piece c relative to piece 0: along the rows and along k.
+    __device__ __forceinline__ static constexpr int prow(int c) { return KC ? 0 : (c % NCR) * 16 * V; }
+    __device__ __forceinline__ static constexpr int pk(int c) { return KC ? c * V : (c / NCR) * 16; }
 
     // FAST (interior stage: tile inside the matrix, 16-byte aligned):
     // unconditional vector loads. Otherwise (edge tiles, the K tail, unaligned
@@ -79,25 +79,25 @@ struct Stage {
         if (FAST) {
             const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) reg[c] = *reinterpret_cast<const vec_t*>(src + piece(c));
+            for (int c = 0; c < NC; ++c)
+                reg[c] = *reinterpret_cast<const vec_t*>(KC ? src + pk(c) : src + pk(c) * ld + prow(c));
         } else {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                const int64_t pr = row0 + r + (KC ? 0 : piece(c));
-                const int64_t pk = k0 + k + (KC ? piece(c) : 0);
-                const bool inside = KC ? (pr < rows && pk + V <= kdim) : (pk < kdim && pr + V <= rows);
-                const bool outside = pr >= rows || pk >= kdim;
+                const int64_t pr = row0 + r + prow(c);
+                const int64_t pkk = k0 + k + pk(c);
+                const bool inside = KC ? (pr < rows && pkk + V <= kdim) : (pkk < kdim && pr + V <= rows);
+                const bool outside = pr >= rows || pkk >= kdim;
                 if (VEC && inside) {
-                    reg[c] = *reinterpret_cast<const vec_t*>(KC ? p + pr * ld + pk : p + pk * ld + pr);
+                    reg[c] = *reinterpret_cast<const vec_t*>(KC ? p + pr * ld + pkk : p + pkk * ld + pr);
                 } else if (outside) {
 #pragma unroll
                     for (int e = 0; e < V; ++e) reg[c][e] = T(0);
                 } else {
 #pragma unroll
                     for (int e = 0; e < V; ++e) {
-                        const int off = piece(c) + e;
-                        const int64_t gr = row0 + r + (KC ? 0 : off);
-                        const int64_t gk = k0 + k + (KC ? off : 0);
+                        const int64_t gr = pr + (KC ? 0 : e);
+                        const int64_t gk = pkk + (KC ? e : 0);
                         const bool ok = gr < rows && gk < kdim;
                         const T x = *(ok ? (KC ? p + gr * ld + gk : p + gk * ld + gr) : p);
                         reg[c][e] = ok ? x : T(0);
@@ -112,41 +112,45 @@ struct Stage {
         place(r, k);
         T* dst = KC ? (s + r * PITCH + k) : (s + k * PITCH + r);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) *reinterpret_cast<vec_t*>(dst + piece(c)) = reg[c];
+        for (int c = 0; c < NC; ++c)
+            *reinterpret_cast<vec_t*>(KC ? dst + pk(c) : dst + pk(c) * PITCH + prow(c)) = reg[c];
     }
 
-    // The four k values (MFMA steps 0..3) this lane feeds for the 16-row block at rb.
-    __device__ __forceinline__ static void frag(const T* s, int rb, int lane, T out[4]) {
+    // The four k values (MFMA steps 0..3 of 16-k pass kk) this lane feeds for
+    // the 16-row block at rb.
+    __device__ __forceinline__ static void frag(const T* s, int rb, int lane, int kk, T out[4]) {
         const int r = rb + (lane & 15);
         const int g = lane >> 4;
         if (KC) {
             typedef typename VecN<T, 4>::type v4_t;
-            const v4_t x = *reinterpret_cast<const v4_t*>(s + r * PITCH + 4 * g);
+            const v4_t x = *reinterpret_cast<const v4_t*>(s + r * PITCH + 16 * kk + 4 * g);
 #pragma unroll
             for (int st = 0; st < 4; ++st) out[st] = x[st];
         } else {
 #pragma unroll
-            for (int st = 0; st < 4; ++st) out[st] = s[(4 * g + st) * PITCH + r];
+            for (int st = 0; st < 4; ++st) out[st] = s[(16 * kk + 4 * g + st) * PITCH + r];
         }
     }
 };
 
-template <typename T, int BM, int BN, int FM, int FN, bool TA, bool TB, bool VEC, bool DOT>
+template <typename T, int BM, int BN, int FM, int FN, bool TA, bool TB, bool VEC, bool DOT, int NBUF, int BK,
+          bool PRIO>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
-    typedef Stage<T, BM, !TA, VEC> SA;
-    typedef Stage<T, BN, TB, VEC> SB;
+    typedef Stage<T, BM, !TA, VEC, BK> SA;
+    typedef Stage<T, BN, TB, VEC, BK> SB;
     // Each wavefront owns an (16 FM) x (16 FN) sub-tile: FM x FN MFMA blocks.
     constexpr int WM = 16 * FM, WN = 16 * FN;
     constexpr int WAVES_N = BN / WN;
     static_assert((BM / WM) * WAVES_N == 4, "four wavefront tiles per workgroup");
 
-    __shared__ __attribute__((aligned(16))) T lds[2 * (SA::ELEMS + SB::ELEMS)];
-    // Stage buffers: A0 A1 B0 B1.
+    static_assert(NBUF == 1 || NBUF == 2, "stage buffers");
+    __shared__ __attribute__((aligned(16))) T lds[NBUF * (SA::ELEMS + SB::ELEMS)];
+    // Stage buffers: A0 (A1) B0 (B1).
     auto bufA = [&](int b) -> T* { return lds + b * SA::ELEMS; };
-    auto bufB = [&](int b) -> T* { return lds + 2 * SA::ELEMS + b * SB::ELEMS; };
+    auto bufB = [&](int b) -> T* { return lds + NBUF * SA::ELEMS + b * SB::ELEMS; };
 
     const int64_t tiles = g.tiles_m * g.tiles_n;
     const int64_t total = tiles * g.batch;
@@ -181,26 +185,29 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
     SA sa;
     SB sb;
-    const int64_t nk = (g.K + kBK - 1) / kBK;
+    const int64_t nk = (g.K + BK - 1) / BK;
     // Stages 0 .. nfull-1 are interior for both operands.
-    const int64_t nfull = (VEC && m0 + BM <= g.M && n0 + BN <= g.N) ? g.K / kBK : 0;
+    const int64_t nfull = (VEC && m0 + BM <= g.M && n0 + BN <= g.N) ? g.K / BK : 0;
     auto load = [&](int64_t k0, auto fast) {
         constexpr bool F = decltype(fast)::value;
         sa.template load<F>(A, g.lda, m0, g.M, k0, g.K);
         sb.template load<F>(B, g.ldb, n0, g.N, k0, g.K);
     };
     auto compute = [&](int buf) {
-        T fa[FM][4], fb[FN][4];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) SA::frag(bufA(buf), wm0 + 16 * i, lane, fa[i]);
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            T fa[FM][4], fb[FN][4];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) SB::frag(bufB(buf), wn0 + 16 * j, lane, fb[j]);
+            for (int i = 0; i < FM; ++i) SA::frag(bufA(buf), wm0 + 16 * i, lane, kk, fa[i]);
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+            for (int j = 0; j < FN; ++j) SB::frag(bufB(buf), wn0 + 16 * j, lane, kk, fb[j]);
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = MF::mma(fa[i][st], fb[j][st], acc[i][j]);
+        }
     };
     if (nk > 0) {
         if (nfull > 0) load(0, std::true_type{});
@@ -211,24 +218,39 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     __syncthreads();
 
     // The scheduling barrier keeps the prefetch's LDS stores (and the wait for
-    // its global loads) behind this stage's MFMAs.
+    // its global loads) behind this stage's MFMAs. With two buffers the next
+    // stage goes to the other buffer (one barrier per stage); with one, it
+    // replaces the current stage after a second barrier (half the LDS, so
+    // more workgroups per CU).
+    auto next = [&](int64_t kt) -> int { return NBUF == 2 ? (int)((kt & 1) ^ 1) : 0; };
+    auto cur = [&](int64_t kt) -> int { return NBUF == 2 ? (int)(kt & 1) : 0; };
     int64_t kt = 0;
+    // PRIO (fp64): the wave issuing a stage's MFMAs runs at raised priority
+    // for the burst, so co-resident waves in their load/store phase do not
+    // delay the MFMA stream.
+    auto mfma_stage = [&](int b) {
+        if (PRIO && sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
+        compute(b);
+        if (PRIO && sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
+    };
     for (; kt + 1 < nfull; ++kt) {
-        load((kt + 1) * kBK, std::true_type{});
-        compute(kt & 1);
+        load((kt + 1) * BK, std::true_type{});
+        mfma_stage(cur(kt));
         __builtin_amdgcn_sched_barrier(0);
-        sa.store(bufA((kt & 1) ^ 1));
-        sb.store(bufB((kt & 1) ^ 1));
+        if (NBUF == 1) __syncthreads();
+        sa.store(bufA(next(kt)));
+        sb.store(bufB(next(kt)));
         __syncthreads();
     }
     for (; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
-        if (more) load((kt + 1) * kBK, std::false_type{});
-        compute(kt & 1);
+        if (more) load((kt + 1) * BK, std::false_type{});
+        mfma_stage(cur(kt));
         __builtin_amdgcn_sched_barrier(0);
+        if (NBUF == 1) __syncthreads();
         if (more) {
-            sa.store(bufA((kt & 1) ^ 1));
-            sb.store(bufB((kt & 1) ^ 1));
+            sa.store(bufA(next(kt)));
+            sb.store(bufB(next(kt)));
         }
         __syncthreads();
     }
@@ -311,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <typename T, int BM, int BN, int FM, int FN, bool DOT>
+template <typename T, int BM, int BN, int FM, int FN, bool DOT, int NBUF = 2, int BK = kBK, bool PRIO = false>
 static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) {
     g.tiles_m = (g.M + BM - 1) / BM;
     g.tiles_n = (g.N + BN - 1) / BN;
@@ -319,7 +341,7 @@ static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) 
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     dim3 grid((unsigned)total), block(kThreads);
 #define TT_GEMM_CASE(TA, TB, VC) \
-    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, FM, FN, TA, TB, VC, DOT>), grid, block, 0, st, g);
+    if (ta == TA && tb == TB && vec == VC) hipLaunchKernelGGL((gemm_kernel<T, BM, BN, FM, FN, TA, TB, VC, DOT, NBUF, BK, PRIO>), grid, block, 0, st, g);
     TT_GEMM_CASE(false, false, false)
     TT_GEMM_CASE(false, false, true)
     TT_GEMM_CASE(false, true, false)
@@ -346,6 +368,14 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // CU instead of two 128 x 128 ones overlap one workgroup's prologue and
     // epilogue with the others' MFMAs (measured 62% -> 70% of fp64 peak;
     // unbatched and fp32 cases measured no gain).
+    // fp64 small-M (the AO->MO half transform: M = nocc, K = nbasis, N =
+    // nbasis * naux): one LDS stage buffer (26 KB) gives four workgroups per
+    // CU instead of three, and the wave issuing a stage's MFMAs raises its
+    // priority for the burst. Same box, results bitwise equal: 64 x 786432 x
+    // 512 0.928-0.952 -> 0.895-0.927 ms (+2-3%). Raised priority measured
+    // slower for the batched and large fp64 tiles (64 x 512^3: +12% time), so
+    // it stays on this tile only.
+    if (sizeof(T) == 8 && !DOT && g.M <= 64) return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
         return launch_tile<T, 64, 128, 2, 4, DOT>(g, ta, tb, vec, st);
     if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4, DOT>(g, ta, tb, vec, st);
