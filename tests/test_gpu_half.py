@@ -89,16 +89,22 @@ def test_dtype_string_bf16_large(hip):
     assert normwise(got.float(), want.float()) <= 1e-2
 
 
-def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=False, seed=0):
+def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=False, seed=0, ld_align=0):
     """tt_gemm with TT_BF16/TT_F16 through engine.gemm against the float64
-    product of the same 16-bit inputs, rounded once to the 16-bit dtype."""
+    product of the same 16-bit inputs, rounded once to the 16-bit dtype.
+    Leading dimensions are the widths plus `pad`, or (ld_align > 0) each width
+    rounded up to a multiple of ld_align."""
     g = torch.Generator().manual_seed(seed)
     dev = torch.device("cuda")
     a_rows, a_cols = (K, M) if ta else (M, K)
     b_rows, b_cols = (N, K) if tb else (K, N)
-    A = torch.randn(batch, a_rows, a_cols + pad, generator=g).to(dt)
-    B = torch.randn(batch, b_rows, b_cols + pad, generator=g).to(dt)
-    C = torch.randn(batch, M, N + pad, generator=g).to(dt)
+    if ld_align:
+        pa, pb, pc = -a_cols % ld_align, -b_cols % ld_align, -N % ld_align
+    else:
+        pa = pb = pc = pad
+    A = torch.randn(batch, a_rows, a_cols + pa, generator=g).to(dt)
+    B = torch.randn(batch, b_rows, b_cols + pb, generator=g).to(dt)
+    C = torch.randn(batch, M, N + pc, generator=g).to(dt)
     opA = A[:, :, :a_cols].double().transpose(1, 2) if ta else A[:, :, :a_cols].double()
     opB = B[:, :, :b_cols].double().transpose(1, 2) if tb else B[:, :, :b_cols].double()
     ref = alpha * torch.bmm(opA, opB)
@@ -106,13 +112,13 @@ def _gemm16_case(dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, alias=F
         ref = ref + beta * C[:, :, :N].double()
     ref = ref.to(dt)
     Ad, Bd, Cd = A.to(dev), B.to(dev), C.to(dev)
-    D = Cd if alias else torch.full((batch, M, N + pad), float("nan"), dtype=dt, device=dev)
+    D = Cd if alias else torch.full((batch, M, N + pc), float("nan"), dtype=dt, device=dev)
     engine.gemm(
         ta, tb, M, N, K,
-        Ad, a_cols + pad, a_rows * (a_cols + pad),
-        Bd, b_cols + pad, b_rows * (b_cols + pad),
-        D, N + pad, M * (N + pad), batch, alpha, beta,
-        Cd if with_c else None, N + pad, M * (N + pad),
+        Ad, a_cols + pa, a_rows * (a_cols + pa),
+        Bd, b_cols + pb, b_rows * (b_cols + pb),
+        D, N + pc, M * (N + pc), batch, alpha, beta,
+        Cd if with_c else None, N + pc, M * (N + pc),
     )
     torch.cuda.synchronize()
     return normwise(D[:, :, :N].float().cpu(), ref.float())
@@ -158,6 +164,18 @@ def test_gemm16_epilogue_alpha_beta(hip, dt, ta, tb, M, N, K, batch, pad):
     smaller shapes run on the register-staged kernel alone."""
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.5, -0.5, True, pad=pad, seed=M) <= BAR[dt]
     assert _gemm16_case(dt, ta, tb, M, N, K, batch, 1.0, 0.0, False, pad=pad, seed=M + 1) <= BAR[dt]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K", [(130, 130, 130), (131, 133, 129), (128, 128, 131), (70, 33, 131)])
+def test_gemm16_aligned_ld_straddling_pieces(hip, dt, ta, tb, M, N, K):
+    """Leading dimensions rounded up to multiples of 8 (16-byte pieces on) with
+    M, N or K not multiples of 8: edge tiles mix whole pieces, pieces outside
+    and pieces straddling the edge."""
+    assert _gemm16_case(dt, ta, tb, M, N, K, 1, 1.0, 0.0, False, ld_align=8, seed=M + N) <= BAR[dt]
+    assert _gemm16_case(dt, ta, tb, M, N, K, 2, 1.5, -0.5, True, ld_align=8, seed=K) <= BAR[dt]
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])

@@ -19,7 +19,10 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float64: 1e-12, torch.float32: 1e-5}
 
 
-def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed=0, alias=False):
+def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed=0, alias=False, ld_align=0):
+    """tt_gemm through engine.gemm against float64 torch. Leading dimensions
+    are the stored widths plus `pad`, or (ld_align > 0) each width rounded up
+    to a multiple of ld_align."""
     from trntensor_amd.hip import engine
 
     g = torch.Generator().manual_seed(seed)
@@ -27,8 +30,10 @@ def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed
     # Stored shapes (row-major) with optional extra columns to exercise ld > width.
     a_rows, a_cols = (K, M) if ta else (M, K)
     b_rows, b_cols = (N, K) if tb else (K, N)
-    A = torch.randn(batch, a_rows, a_cols + pad, generator=g, dtype=torch.float64)
-    B = torch.randn(batch, b_rows, b_cols + pad, generator=g, dtype=torch.float64)
+    lda = a_cols + (-a_cols % ld_align if ld_align else pad)
+    ldb = b_cols + (-b_cols % ld_align if ld_align else pad)
+    A = torch.randn(batch, a_rows, lda, generator=g, dtype=torch.float64)
+    B = torch.randn(batch, b_rows, ldb, generator=g, dtype=torch.float64)
     C = torch.randn(batch, M, N, generator=g, dtype=torch.float64)
     opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
     opB = B[:, :, :b_cols].transpose(1, 2) if tb else B[:, :, :b_cols]
@@ -39,13 +44,27 @@ def _gemm_case(hip, dt, ta, tb, M, N, K, batch, alpha, beta, with_c, pad=0, seed
     D = Cd if alias else torch.full((batch, M, N), float("nan"), dtype=dt, device=dev)
     engine.gemm(
         ta, tb, M, N, K,
-        Ad, a_cols + pad, a_rows * (a_cols + pad),
-        Bd, b_cols + pad, b_rows * (b_cols + pad),
+        Ad, lda, a_rows * lda,
+        Bd, ldb, b_rows * ldb,
         D, N, M * N, batch, alpha, beta,
         Cd if with_c else None, N, M * N,
     )
     torch.cuda.synchronize()
     return normwise(D, ref)
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K", [(130, 130, 130), (131, 131, 131), (128, 128, 131), (131, 128, 128), (128, 131, 128),
+                                   (70, 33, 131)])
+def test_gemm_aligned_ld_straddling_pieces(hip, dt, ta, tb, M, N, K):
+    """Leading dimensions rounded up to multiples of 8 (16-byte vector path on)
+    with M, N or K not multiples of the vector width: edge tiles mix whole
+    vector pieces, pieces outside (zero, no load) and pieces that straddle
+    the edge (element loads)."""
+    assert _gemm_case(hip, dt, ta, tb, M, N, K, 1, 1.0, 0.0, False, ld_align=8, seed=M + N + K) <= TOL[dt]
+    assert _gemm_case(hip, dt, ta, tb, M, N, K, 2, 1.5, -0.5, True, ld_align=8, seed=M + 7) <= TOL[dt]
 
 
 @pytest.mark.parametrize("dt", [torch.float64, torch.float32])
