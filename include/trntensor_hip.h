@@ -19,7 +19,9 @@
  *    exactly and summed in double-double (Ogita-Rump-Oishi Dot2), rounded
  *    to double once per output. TT_BF16 = 3, TT_F16 = 4 (tt_gemm only):
  *    16-bit A, B, C, D; products and sums in fp32 on the 16-bit MFMA, alpha
- *    and beta applied in fp32, one rounding at the store.
+ *    and beta applied in fp32, one rounding at the store. TT_I64 = 5
+ *    (tt_strided_contract only): int64 data, products and sums with
+ *    two's-complement wraparound, integral alpha and beta.
  *  - Return codes: TT_OK 0; TT_INVALID 1 (bad argument: the Python layer
  *    raises ValueError); TT_UNSUPPORTED 2 (dtype/shape the kernels do not
  *    cover: NotImplementedError); TT_HIP_ERROR 3 (launch failure:
@@ -36,11 +38,11 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 2
+#define TT_ABI_VERSION 3
 #define TT_MAX_DIMS 8
 
 enum { TT_OK = 0, TT_INVALID = 1, TT_UNSUPPORTED = 2, TT_HIP_ERROR = 3 };
-enum { TT_F32 = 0, TT_F64 = 1, TT_F64_DD = 2, TT_BF16 = 3, TT_F16 = 4 };
+enum { TT_F32 = 0, TT_F64 = 1, TT_F64_DD = 2, TT_BF16 = 3, TT_F16 = 4, TT_I64 = 5 };
 
 /* ABI version of the loaded library (TT_ABI_VERSION at build time). */
 int tt_abi_version(void);
@@ -185,7 +187,10 @@ size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, const int64_t* 
  * given element strides (0 broadcasts). B may be NULL (single operand:
  * the factor is 1). D and C are contiguous in out_shape order; C is read iff
  * non-NULL. Accumulation is in `dtype`; TT_F64_DD accumulates double data
- * in double-double (partial sums travel as pairs) and rounds once.
+ * in double-double (partial sums travel as pairs) and rounds once. TT_I64
+ * accumulates int64 with wraparound (so any integer dtype widened to int64
+ * and truncated back equals its own wrapping accumulation); it requires
+ * integral alpha and beta (TT_INVALID otherwise).
  *
  * No counterpart kernel in the reference: these contractions are the
  * "torch" strategy, which the reference hands to torch.einsum

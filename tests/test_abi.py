@@ -145,3 +145,12 @@ def test_fast_division_formula():
                 continue
             q = (((n * m) >> 32) + n) >> s
             assert q == n // d, (n, d)
+
+
+def test_strided_int64_needs_integral_scalars(lib):
+    dummy = ctypes.c_void_p(256)
+    shape = _lib.i64_array([4])
+    st = lib.tt_strided_contract(_lib.TT_I64, 1, shape, shape, shape, 0, shape, shape, shape, dummy, None, 1.5, 0.0, None, dummy, None, 0, None)
+    assert st == _lib.TT_INVALID and b"integral" in lib.tt_last_error()
+    st = lib.tt_strided_contract(_lib.TT_I64, 1, shape, shape, shape, 0, shape, shape, shape, dummy, None, 1.0, 0.25, None, dummy, None, 0, None)
+    assert st == _lib.TT_INVALID

@@ -450,3 +450,102 @@ class TestOptimalPath:
         # |sum| bound: the same contraction over absolute values, via the cheap order
         scale = trntensor.einsum("ia,jb,abP,ijP->", A.abs(), B.abs(), W.abs(), V.abs(), optimize="optimal")
         assert abs(float(fast) - float(slow)) <= 1e-13 * float(scale)
+
+
+class TestIntegerAndComplex:
+    """Non-floating operands, which the reference hands to torch.einsum /
+    torch.matmul (trntensor/einsum.py:117-118, nki/dispatch.py:195-196).
+    Integers: int64 accumulation with wraparound on the strided kernel,
+    truncated to the operands' dtype: equal element for element to the
+    oracle's int64 contraction truncated the same way, and to the oracle
+    itself wherever torch keeps the narrow dtype (torch promotes some
+    narrow-integer reductions to int64 through torch.sum, depending on the
+    pattern and the extents). Complex: real contractions of the parts on the
+    MFMA core; normwise bars of the parts' dtype."""
+
+    PATTERNS = [
+        ("ij,jk->ik", [(37, 50), (50, 29)]),
+        ("ij,kj->ik", [(37, 50), (29, 50)]),
+        ("bij,bjk->bik", [(3, 20, 30), (3, 30, 10)]),
+        ("mi,mnP->inP", [(12, 5), (12, 12, 7)]),
+        ("ii->", [(9, 9)]),
+        ("i,j->ij", [(6,), (8,)]),
+        ("ijk->k", [(5, 6, 70)]),
+        ("ij,jk,kl->il", [(5, 8), (8, 6), (6, 4)]),
+        ("ia,jb,abP,ijP->", [(4, 5), (3, 6), (5, 6, 7), (4, 3, 7)]),
+    ]
+
+    @pytest.mark.parametrize("dt", [torch.int64, torch.int32, torch.int16, torch.int8, torch.uint8])
+    @pytest.mark.parametrize("sub,shapes", PATTERNS)
+    def test_integers_equal_oracle(self, hip, dt, sub, shapes):
+        g = torch.Generator().manual_seed(len(sub) + len(shapes))
+        lo, hi = (0, 256) if dt == torch.uint8 else (-120, 120)
+        if dt == torch.int64:
+            lo, hi = -(1 << 40), 1 << 40  # products and sums wrap modulo 2^64
+        ops = [torch.randint(lo, hi, s, generator=g, dtype=torch.int64).to(dt) for s in shapes]
+        want = cpu_ref.einsum(sub, *[o.to(torch.int64) for o in ops]).to(dt)
+        got = trntensor.einsum(sub, *[o.cuda() for o in ops])
+        assert got.dtype == dt and got.device.type == "cuda"
+        assert torch.equal(got.cpu(), want), (got.cpu().long() - want.long()).abs().max()
+        ref = cpu_ref.einsum(sub, *ops)
+        if ref.dtype == dt:
+            assert torch.equal(got.cpu(), ref)
+
+    def test_integer_alpha_beta_semantics(self, hip):
+        g = torch.Generator().manual_seed(3)
+        A, B = (torch.randint(-50, 50, s, generator=g) for s in [(20, 30), (30, 10)])
+        out = torch.randint(-50, 50, (20, 10), generator=g)
+        for kw in ({"alpha": 2}, {"alpha": 1.5}, {"beta": 3, "out": out}, {"alpha": 2, "beta": -1, "out": out},
+                   {"alpha": 0.5, "beta": 2, "out": out}, {"beta": 2, "out": out.double()}):
+            ref = cpu_ref.einsum("ij,jk->ik", A, B, **kw)
+            got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), **{k: (v.cuda() if torch.is_tensor(v) else v) for k, v in kw.items()})
+            assert got.dtype == ref.dtype, kw
+            assert torch.equal(got.cpu(), ref), kw
+        # an integral result takes only an integral beta (torch's rule)
+        with pytest.raises(RuntimeError, match="integral"):
+            cpu_ref.einsum("ij,jk->ik", A, B, beta=0.5, out=out)
+        with pytest.raises(RuntimeError, match="integral"):
+            trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), beta=0.5, out=out.cuda())
+
+    @pytest.mark.parametrize("dt", [torch.complex128, torch.complex64])
+    @pytest.mark.parametrize("sub,shapes", PATTERNS)
+    def test_complex_matches_oracle(self, hip, dt, sub, shapes):
+        g = torch.Generator().manual_seed(len(sub) * 3 + len(shapes))
+        ops = [torch.randn(*s, generator=g, dtype=torch.complex128).to(dt) for s in shapes]
+        ref = cpu_ref.einsum(sub, *ops)
+        got = trntensor.einsum(sub, *[o.cuda() for o in ops])
+        assert got.dtype == ref.dtype == dt
+        bar = 1e-12 if dt == torch.complex128 else 1e-5
+        assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= bar
+
+    @pytest.mark.parametrize("dt", [torch.complex128, torch.complex64])
+    def test_complex_alpha_beta_out(self, hip, dt):
+        g = torch.Generator().manual_seed(8)
+        A = torch.randn(40, 30, generator=g, dtype=torch.complex128).to(dt)
+        B = torch.randn(30, 20, generator=g, dtype=torch.complex128).to(dt)
+        outc = torch.randn(40, 20, generator=g, dtype=torch.complex128).to(dt)
+        outr = torch.randn(1, 20, generator=g, dtype=torch.float64)
+        bar = 1e-12 if dt == torch.complex128 else 1e-5
+        for kw in ({"alpha": 1.5}, {"alpha": 1 - 2j}, {"beta": 0.5, "out": outc}, {"alpha": 2j, "beta": 0.5 + 1j, "out": outc},
+                   {"beta": -1.0, "out": outr}):
+            ref = cpu_ref.einsum("ij,jk->ik", A, B, **kw)
+            got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), **{k: (v.cuda() if torch.is_tensor(v) else v) for k, v in kw.items()})
+            assert got.dtype == ref.dtype and got.shape == ref.shape, kw
+            assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= bar, kw
+
+    def test_real_operands_complex_out(self, hip):
+        g = torch.Generator().manual_seed(9)
+        A, B = torch.randn(16, 24, generator=g), torch.randn(24, 8, generator=g)
+        out = torch.randn(16, 8, generator=g, dtype=torch.complex64)
+        ref = cpu_ref.einsum("ij,jk->ik", A, B, alpha=2.0, beta=1 + 1j, out=out)
+        got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), alpha=2.0, beta=1 + 1j, out=out.cuda())
+        assert got.dtype == ref.dtype == torch.complex64
+        assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= 1e-5
+
+    def test_conjugate_view_operand(self, hip):
+        g = torch.Generator().manual_seed(10)
+        A = torch.randn(12, 9, generator=g, dtype=torch.complex128)
+        B = torch.randn(9, 7, generator=g, dtype=torch.complex128)
+        ref = cpu_ref.einsum("ij,jk->ik", A.conj(), B)
+        got = trntensor.einsum("ij,jk->ik", A.cuda().conj(), B.cuda())
+        assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= 1e-12

@@ -312,3 +312,21 @@ class TestExactEinsum:
             exact = sum((Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x, y)), Fraction(0))
             cond = 2 * float(np.sum(np.abs(x * y))) / abs(float(exact))
             assert 10 ** (logc - 3) <= cond <= 10 ** (logc + 4), (logc, cond)
+
+
+def test_integer_einsum_wraps_like_int64_truncated():
+    """The integer path computes in int64 (wrapping) and truncates to the
+    operands' dtype. Pinned: the oracle's (torch's) int8 and int32 einsums
+    equal the int64 contraction reduced modulo 2^8 / 2^32, including sums
+    that overflow the narrow type."""
+    g = torch.Generator().manual_seed(4)
+    for dt, bits in ((torch.int8, 8), (torch.int32, 32)):
+        lo, hi = (-128, 128) if bits == 8 else (-(1 << 31), 1 << 31)
+        A = torch.randint(lo, hi, (20, 300), generator=g, dtype=torch.int64)
+        B = torch.randint(lo, hi, (300, 10), generator=g, dtype=torch.int64)
+        wide = np.einsum("ij,jk->ik", A.numpy().astype(object), B.numpy().astype(object))
+        want = np.vectorize(lambda v: ((v + (1 << (bits - 1))) % (1 << bits)) - (1 << (bits - 1)))(wide).astype(np.int64)
+        got = cpu_ref.einsum("ij,jk->ik", A.to(dt), B.to(dt))
+        assert got.dtype == dt
+        assert np.array_equal(got.to(torch.int64).numpy(), want)
+        assert np.abs(wide).max() >= (1 << (bits - 1)), "the data must overflow the narrow type"

@@ -83,6 +83,35 @@ struct Acc<T, false> {
     __device__ __forceinline__ T value() const { return v; }
 };
 
+// int64: two's-complement wraparound (unsigned arithmetic), so every
+// integer dtype computed through int64 and truncated back equals its own
+// wrapping accumulation. Wave totals travel bit-exactly through the double
+// scratch slots.
+template <>
+struct Acc<int64_t, false> {
+    uint64_t v = 0;
+    __device__ __forceinline__ void add_prod(int64_t x, int64_t y) { v += (uint64_t)x * (uint64_t)y; }
+    __device__ __forceinline__ void add(int64_t x) { v += (uint64_t)x; }
+    __device__ __forceinline__ void wave_reduce() {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += (uint64_t)__shfl_xor((long long)v, off, 64);
+    }
+    __device__ __forceinline__ void put(double* red, int w) const { red[w] = __longlong_as_double((long long)v); }
+    __device__ __forceinline__ void take4(const double* red) {
+        v = ((uint64_t)__double_as_longlong(red[0]) + (uint64_t)__double_as_longlong(red[1])) +
+            ((uint64_t)__double_as_longlong(red[2]) + (uint64_t)__double_as_longlong(red[3]));
+    }
+    __device__ __forceinline__ void store_partial(void* P, int64_t idx, int64_t plane) const {
+        (void)plane;
+        static_cast<int64_t*>(P)[idx] = (int64_t)v;
+    }
+    __device__ __forceinline__ void add_partial(const void* P, int64_t idx, int64_t plane) {
+        (void)plane;
+        v += (uint64_t) static_cast<const int64_t*>(P)[idx];
+    }
+    __device__ __forceinline__ int64_t value() const { return (int64_t)v; }
+};
+
 template <>
 struct Acc<double, true> : Dot2 {
     __device__ __forceinline__ void wave_reduce() {
@@ -146,11 +175,28 @@ __device__ __forceinline__ void reduce_range(Acc<T, DD>& acc, const T* __restric
     }
 }
 
+// alpha * v (+ beta * c). For int64 the host admits only integral alpha and
+// beta, applied with wraparound.
+__device__ __forceinline__ int64_t scale(int64_t v, double alpha) {
+    return (int64_t)((uint64_t)v * (uint64_t)(int64_t)alpha);
+}
+template <typename T>
+__device__ __forceinline__ T scale(T v, double alpha) {
+    return (T)alpha * v;
+}
+__device__ __forceinline__ int64_t add_scaled(int64_t v, double beta, int64_t c) {
+    return (int64_t)((uint64_t)v + (uint64_t)(int64_t)beta * (uint64_t)c);
+}
+template <typename T>
+__device__ __forceinline__ T add_scaled(T v, double beta, T c) {
+    return v + (T)beta * c;
+}
+
 template <typename T, bool DD>
 __device__ __forceinline__ T finish(const StridedArgs& g, int64_t o, const Acc<T, DD>& acc) {
     T v = acc.value();
-    if (g.alpha != 1.0) v = (T)g.alpha * v;
-    if (g.C) v = v + (T)g.beta * static_cast<const T*>(g.C)[o];
+    if (g.alpha != 1.0) v = scale(v, g.alpha);
+    if (g.C) v = add_scaled(v, g.beta, static_cast<const T*>(g.C)[o]);
     return v;
 }
 
@@ -287,8 +333,8 @@ __global__ __launch_bounds__(256) void strided_transpose_kernel(StridedArgs g, T
         const int64_t u = u0 + lo, v = v0 + vl;
         if (u < t.U && v < t.V) {
             T y = tile[lo][vl];
-            if (g.alpha != 1.0) y = (T)g.alpha * y;
-            if (C) y = y + (T)g.beta * c[i];
+            if (g.alpha != 1.0) y = scale(y, g.alpha);
+            if (C) y = add_scaled(y, g.beta, c[i]);
             D[zd + v * t.sd_v + u] = y;
         }
     }
@@ -420,7 +466,7 @@ extern "C" size_t tt_strided_contract_workspace_bytes(int dtype, int n_out, cons
     }
     if (parts <= 1) return 0;
     // TT_F64_DD partials are (p, s) pairs of doubles.
-    const size_t es = dtype == TT_F64_DD ? 16 : dtype == TT_F64 ? 8 : 4;
+    const size_t es = dtype == TT_F64_DD ? 16 : (dtype == TT_F64 || dtype == TT_I64) ? 8 : 4;
     return ((size_t)(parts * no) * es + 255) / 256 * 256;
 }
 
@@ -432,8 +478,15 @@ extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shap
     using namespace tt;
     if (n_out < 0 || n_red < 0 || n_out > TT_MAX_DIMS || n_red > TT_MAX_DIMS)
         return set_error(TT_INVALID, "tt_strided_contract: dims out=%d red=%d (max %d)", n_out, n_red, TT_MAX_DIMS);
-    if (dtype != TT_F32 && dtype != TT_F64 && dtype != TT_F64_DD)
-        return set_error(TT_UNSUPPORTED, "tt_strided_contract: dtype %d (only TT_F32, TT_F64, TT_F64_DD)", dtype);
+    if (dtype != TT_F32 && dtype != TT_F64 && dtype != TT_F64_DD && dtype != TT_I64)
+        return set_error(TT_UNSUPPORTED, "tt_strided_contract: dtype %d (only TT_F32, TT_F64, TT_F64_DD, TT_I64)",
+                         dtype);
+    if (dtype == TT_I64) {
+        auto integral = [](double x) { return x >= -9.2e18 && x <= 9.2e18 && x == (double)(int64_t)x; };
+        if (!integral(alpha) || !integral(beta))
+            return set_error(TT_INVALID, "tt_strided_contract: TT_I64 takes integral alpha and beta (got %g, %g)",
+                             alpha, beta);
+    }
     for (int k = 0; k < n_out; ++k)
         if (out_shape[k] < 0) return set_error(TT_INVALID, "tt_strided_contract: negative output extent");
     for (int k = 0; k < n_red; ++k)
@@ -477,5 +530,6 @@ extern "C" int tt_strided_contract(int dtype, int n_out, const int64_t* out_shap
     }
     if (dtype == TT_F64_DD) return run_typed<double, true>(g, out_shape, st);
     if (dtype == TT_F64) return run_typed<double, false>(g, out_shape, st);
+    if (dtype == TT_I64) return run_typed<int64_t, false>(g, out_shape, st);
     return run_typed<float, false>(g, out_shape, st);
 }

@@ -120,6 +120,19 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
     lhs, out_str = _parse_subscripts(subscripts)
     terms = lhs.split(",")
 
+    prefer_gemm = plan.strategy in ("matmul", "bmm")
+    if res_dtype.is_complex or not res_dtype.is_floating_point:
+        # Integer and complex results: the contraction alone on the kernels,
+        # then the reference's two scalar passes (trntensor/einsum.py:99-102)
+        # under torch's promotion rules: an integer result times a float
+        # alpha becomes float32, complex scalars rotate the parts, an integral
+        # result takes only an integral beta.
+        res = _contract(terms, out_str, ops, plan, 1.0, 0.0, None, prefer_gemm)
+        if res.dtype != res_dtype:
+            res = res.to(res_dtype)
+        res = _scalar_epilogue(res, alpha, beta, out_dev)
+        return res if res.device == orig else res.to(orig)
+
     # The reference finishes with result.add(out, alpha=beta)
     # (trntensor/einsum.py:101-102): torch's type promotion and broadcasting.
     # When `out` promotes to the contraction's dtype and broadcasts to its
@@ -139,30 +152,88 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
             post = (final_dtype, final_shape)
 
     kb, kc = (beta, C) if post is None else (0.0, None)
-    if plan.strategy == "path":
-        res = _execute_path(terms, out_str, ops, plan.contraction_path, alpha, kb, kc)
-    else:
-        res = engine.contract(
-            terms, out_str, ops, alpha, kb, kc, prefer_gemm=plan.strategy in ("matmul", "bmm")
-        )
+    res = _contract(terms, out_str, ops, plan, alpha, kb, kc, prefer_gemm)
     if res.dtype != res_dtype:
         res = res.to(res_dtype)
     if post is not None:
-        res = _add_out(res, out_dev, beta, *post)
+        res = _scalar_epilogue(res, 1.0, beta, out_dev)
     return res if res.device == orig else res.to(orig)
 
 
-def _add_out(res: torch.Tensor, out: torch.Tensor, beta: float, dtype: torch.dtype, shape: list[int]) -> torch.Tensor:
-    """res + beta * out in `dtype`, broadcast to `shape` (one strided pass on the
-    device; 16-bit results are computed in float32 and rounded once)."""
+def _contract(terms, out_str, ops, plan, alpha, beta, C, prefer_gemm):
+    if plan.strategy == "path":
+        return _execute_path(terms, out_str, ops, plan.contraction_path, alpha, beta, C)
+    return engine.contract(terms, out_str, ops, alpha, beta, C, prefer_gemm=prefer_gemm)
+
+
+def _scalar_epilogue(res: torch.Tensor, alpha, beta, out: torch.Tensor | None) -> torch.Tensor:
+    """result.mul(alpha) if alpha != 1, then result.add(out, alpha=beta), with
+    torch's dtype rules (trntensor/einsum.py:99-102), on the device kernels."""
+    if alpha != 1.0:
+        res = _mul_scalar(res, alpha)
+    if out is None:
+        return res
+    dtype = torch.promote_types(res.dtype, out.dtype)
+    if not (dtype.is_floating_point or dtype.is_complex) and isinstance(beta, float):
+        raise RuntimeError("For integral input tensors, argument alpha must not be a floating point number.")
+    if not dtype.is_complex and isinstance(beta, complex):
+        raise RuntimeError("For non-complex input tensors, argument alpha must not be a complex number.")
+    shape = list(torch.broadcast_shapes(tuple(res.shape), tuple(out.shape)))
+    return _add_out(res, out, beta, dtype, shape)
+
+
+def _mul_scalar(res: torch.Tensor, alpha) -> torch.Tensor:
+    """res * alpha in torch.result_type(res, alpha), one strided pass per part."""
+    dtype = torch.result_type(res, alpha)
+    if dtype.is_complex:
+        re, im = engine.complex_parts(res.to(dtype).resolve_conj())
+        a = complex(alpha)
+        if a.imag == 0:
+            re2, im2 = _axpby(re, a.real), _axpby(im, a.real)
+        else:
+            # (re + i im)(ar + i ai) = (ar re - ai im) + i (ar im + ai re)
+            re2, im2 = _axpby(re, a.real, im, -a.imag), _axpby(im, a.real, re, a.imag)
+        return torch.complex(re2, im2)
     cd = dispatch.compute_dtype(dtype)
-    r = res.to(cd)
+    r = res.to(cd).contiguous()
+    out = _axpby(r, int(alpha) if cd == torch.int64 else float(alpha))
+    return out if cd == dtype else out.to(dtype)
+
+
+def _axpby(x: torch.Tensor, a, y: torch.Tensor | None = None, b=0.0) -> torch.Tensor:
+    """a * x (+ b * y) for contiguous real tensors of one shape (one strided pass)."""
+    D = torch.empty_like(x)
+    engine.strided_contract([(n, s, 0) for n, s in zip(x.shape, x.stride())], [], x, None, D, a, b, y)
+    return D
+
+
+def _add_out(res: torch.Tensor, out: torch.Tensor, beta, dtype: torch.dtype, shape: list[int]) -> torch.Tensor:
+    """res + beta * out in `dtype`, broadcast to `shape` (one strided pass on the
+    device per real part; 16-bit results are computed in float32 and rounded
+    once; integers in int64 with wraparound)."""
+    if dtype.is_complex:
+        rr, ri = engine.complex_parts(res.to(dtype).resolve_conj())
+        orr, ori = engine.complex_parts(out.to(dtype).resolve_conj())
+        b = complex(beta)
+        re = _add_real(rr, orr, b.real, shape)
+        im = _add_real(ri, ori, b.real, shape)
+        if b.imag != 0:
+            re = _add_real(re, ori, -b.imag, shape)
+            im = _add_real(im, orr, b.imag, shape)
+        return torch.complex(re, im)
+    cd = dispatch.compute_dtype(dtype)
+    D = _add_real(res.to(cd), out.to(cd), int(beta) if cd == torch.int64 else beta, shape)
+    return D if cd == dtype else D.to(dtype)
+
+
+def _add_real(r: torch.Tensor, o: torch.Tensor, beta, shape: list[int]) -> torch.Tensor:
+    """r + beta * o, both broadcast to `shape`, in their (common, real) dtype."""
     lead = len(shape) - r.dim()
     strides = [0] * lead + [0 if n == 1 and m != 1 else s for n, m, s in zip(r.shape, shape[lead:], r.stride())]
-    C = out.to(cd).expand(shape).contiguous()
-    D = torch.empty(shape, dtype=cd, device=res.device)
+    C = o.expand(shape).contiguous()
+    D = torch.empty(shape, dtype=r.dtype, device=r.device)
     engine.strided_contract([(n, s, 0) for n, s in zip(shape, strides)], [], r, None, D, 1.0, beta, C)
-    return D if cd == dtype else D.to(dtype)
+    return D
 
 
 def _result_shape(terms, out_str, ops) -> list[int]:
@@ -292,8 +363,9 @@ def _execute_path(
     outer product of 'ia,jb,abP,ijP->' are never written.
     """
     names = _path_names(terms, out, path)
-    # The fused dot epilogue accumulates in float64 only.
-    plan = None if engine._ACCUMULATION.get() == "dd" else _fusion_plan(terms, out, path, names)
+    # The fused dot epilogue covers real float32/float64 products with native accumulation.
+    fusable = engine._ACCUMULATION.get() != "dd" and ops[0].dtype in (torch.float32, torch.float64)
+    plan = _fusion_plan(terms, out, path, names) if fusable else None
     deferred = set() if plan is None else {s for s in plan if s is not None}
     cur_terms = list(terms)
     cur: list = list(ops)

@@ -15,9 +15,9 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib", "libtrntensor_hip.so")
 
 TT_OK, TT_INVALID, TT_UNSUPPORTED, TT_HIP_ERROR = 0, 1, 2, 3
-TT_F32, TT_F64, TT_F64_DD, TT_BF16, TT_F16 = 0, 1, 2, 3, 4
+TT_F32, TT_F64, TT_F64_DD, TT_BF16, TT_F16, TT_I64 = 0, 1, 2, 3, 4, 5
 TT_MAX_DIMS = 8
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/trntensor_hip.h declares, with its ctypes signature.
 _i64 = ctypes.c_int64

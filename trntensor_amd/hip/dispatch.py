@@ -150,15 +150,21 @@ def place(*tensors: torch.Tensor) -> tuple[list[torch.Tensor], torch.device]:
 
 
 _WIDEN = {torch.bfloat16: torch.float32, torch.float16: torch.float32}
+_INTS = (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8)
 
 
 def compute_dtype(dt: torch.dtype) -> torch.dtype:
-    """Kernel dtype for an operand dtype: fp32/fp64 as is, bf16/fp16 widened to fp32
-    (exact; products of 8/11-bit mantissas are exact in fp32 accumulation)."""
-    if dt in (torch.float32, torch.float64):
+    """Kernel dtype for an operand dtype: fp32/fp64 and complex64/complex128 as
+    is (complex contractions run as real ones on their parts), bf16/fp16
+    widened to fp32 (exact; products of 8/11-bit mantissas are exact in fp32
+    accumulation), integers widened to int64 (sums wrap modulo 2^64, so
+    truncating back gives each type's own wrapping result)."""
+    if dt in (torch.float32, torch.float64, torch.complex64, torch.complex128):
         return dt
     if dt in _WIDEN:
         return _WIDEN[dt]
+    if dt in _INTS:
+        return torch.int64
     raise NotImplementedError(f"trntensor_amd HIP kernels do not compute in {dt}")
 
 

@@ -64,7 +64,9 @@ def dtype_code(dt: torch.dtype) -> int:
         return _lib.TT_BF16
     if dt == torch.float16:
         return _lib.TT_F16
-    raise NotImplementedError(f"HIP kernels compute in float32/float64 (bfloat16/float16 GEMMs), not {dt}")
+    if dt == torch.int64:
+        return _lib.TT_I64
+    raise NotImplementedError(f"HIP kernels compute in float32/float64 (bfloat16/float16 GEMMs, int64 strided), not {dt}")
 
 
 # Raw handle of torch's current stream on a device index (what
@@ -678,6 +680,8 @@ def contract(
     contraction maps onto it without packing; otherwise they are widened to
     float32 (exactly) and the result is rounded back to their dtype.
     """
+    if tensors[0].is_complex():
+        return _contract_complex(terms, out, tensors, alpha, beta, C, prefer_gemm)
     key = None
     if len(tensors) == 2:
         a, b = tensors
@@ -719,7 +723,8 @@ def contract(
         # rounded to float64 before the GEMM; such contractions take the
         # strided kernel, which accumulates the whole reduction in one pair.
         one_sided = any(c not in lb and c not in lo for c in la) or any(c not in la and c not in lo for c in lb)
-        if kl and not (one_sided and _ACCUMULATION.get() == "dd"):
+        # Integer contractions take the strided kernel (int64, wrapping sums).
+        if kl and not (one_sided and _ACCUMULATION.get() == "dd") and dt != torch.int64:
             M = _numel(ext[c] for c in ml)
             N = _numel(ext[c] for c in nl)
             if prefer_gemm or (M >= 16 and N >= 16):
@@ -764,6 +769,44 @@ def contract(
         C,
     )
     return D
+
+
+# ---------------------------------------------------------------------------
+# complex operands: real contractions on the parts
+# ---------------------------------------------------------------------------
+def complex_parts(z: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(real, imaginary) parts of a complex tensor as contiguous real tensors
+    (one strided copy each, on the device)."""
+    v = torch.view_as_real(z.resolve_conj())
+    parts = []
+    for k in (0, 1):
+        P = torch.empty(z.shape, dtype=v.dtype, device=z.device)
+        strided_contract([(n, s, 0) for n, s in zip(z.shape, v.stride()[:-1])], [], v, None, P, a_off=k)
+        parts.append(P)
+    return parts[0], parts[1]
+
+
+def _contract_complex(terms, out, tensors, alpha, beta, C, prefer_gemm):
+    """A complex contraction as real ones: one operand contracts each part;
+    two operands give Re = ArBr - AiBi and Im = ArBi + AiBr, the second
+    product of each added through the first's beta epilogue. alpha and beta
+    are real here (complex scalars are applied by the caller); C (complex,
+    contiguous in the output's shape) enters as beta * C."""
+    if isinstance(alpha, complex) or isinstance(beta, complex):
+        raise NotImplementedError("complex alpha/beta are applied outside the engine")
+    parts = [complex_parts(t) for t in tensors]
+    Cr, Ci = complex_parts(C) if C is not None else (None, None)
+    if len(tensors) == 1:
+        (ar, ai), = parts
+        re = contract(terms, out, [ar], alpha, beta, Cr)
+        im = contract(terms, out, [ai], alpha, beta, Ci)
+    else:
+        (ar, ai), (br, bi) = parts
+        re = contract(terms, out, [ar, br], alpha, beta, Cr, prefer_gemm)
+        re = contract(terms, out, [ai, bi], -alpha, 1.0, re, prefer_gemm)
+        im = contract(terms, out, [ar, bi], alpha, beta, Ci, prefer_gemm)
+        im = contract(terms, out, [ai, br], alpha, 1.0, im, prefer_gemm)
+    return torch.complex(re, im)
 
 
 # ---------------------------------------------------------------------------
