@@ -74,6 +74,24 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
+// Thread t's sum of p[t], p[t + 256], p[t + 512], ... (< n), in that order.
+// Eight loads are issued before their sums (the order of the sums is
+// unchanged): a single workgroup walking tens of thousands of partials with
+// one load in flight per thread waits out a memory latency per element.
+__device__ __forceinline__ double strided_sum256(const double* __restrict__ p, int64_t n) {
+    double s = 0.0;
+    int64_t k = threadIdx.x;
+    for (; k + 7 * 256 < n; k += 8 * 256) {
+        double x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = p[k + u * 256];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += x[u];
+    }
+    for (; k < n; k += 256) s += p[k];
+    return s;
+}
+
 // Sum over a 256-thread block; result valid in thread 0. `scratch` holds >= 4 doubles.
 __device__ __forceinline__ double block256_sum(double v, double* scratch) {
     v = wave_sum(v);

@@ -414,8 +414,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void dot_finalize_kernel(const double* partial, int64_t n, double alpha, double beta,
                                                            const T* C, T* out) {
     __shared__ double red[4];
-    double s = 0.0;
-    for (int64_t k = threadIdx.x; k < n; k += 256) s += partial[k];
+    const double s = strided_sum256(partial, n);
     const double tot = block256_sum(s, red);
     if (threadIdx.x == 0) {
         T v = (T)tot;

@@ -381,8 +381,7 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
 template <typename T>
 __global__ __launch_bounds__(256) void mp2_finalize_kernel(const double* partial, int64_t n, T* out) {
     __shared__ double red[4];
-    double s = 0.0;
-    for (int64_t k = threadIdx.x; k < n; k += 256) s += partial[k];
+    const double s = strided_sum256(partial, n);
     double tot = block256_sum(s, red);
     if (threadIdx.x == 0) out[0] = (T)tot;
 }
