@@ -154,3 +154,24 @@ def test_strided_int64_needs_integral_scalars(lib):
     assert st == _lib.TT_INVALID and b"integral" in lib.tt_last_error()
     st = lib.tt_strided_contract(_lib.TT_I64, 1, shape, shape, shape, 0, shape, shape, shape, dummy, None, 1.0, 0.25, None, dummy, None, 0, None)
     assert st == _lib.TT_INVALID
+
+
+def test_plain_c_client_compiles_links_and_runs(tmp_path):
+    """tests/c_abi/abi_smoke.c: the header compiles as C (gcc -std=c99), the
+    program links against the built library and its host-side checks pass."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    src = os.path.join(ROOT, "tests", "c_abi", "abi_smoke.c")
+    exe = str(tmp_path / "abi_smoke")
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    cmd = [gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), src, "-o", exe,
+           "-L", libdir, "-ltrntensor_hip", f"-Wl,-rpath,{libdir}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    run = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "c abi ok" in run.stdout
