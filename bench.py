@@ -466,6 +466,18 @@ def bench_c4_naux(torch, tt, dev, args):
             out[f"{key}_naux{naux}"] = {"ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                                         "frac_mfma": round(flop / (ms * 1e-3) / peak, 4)}
             del B, eo, ev
+    # One GPU's share of an 8-GPU run at config 4 (fp64): each shard is a
+    # contiguous eighth of the 31,200 work units (tt_mp2_energy_shard).
+    print("bench: c4 shards of 8", file=sys.stderr, flush=True)
+    B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, torch.float64))
+    shard_ms = []
+    for r in range(8):
+        _, ms = timed_steady(torch, lambda: tt.mp2_energy_shard(B, eo, ev, r, 8), max(5, args.steps))
+        shard_ms.append(ms)
+    _, whole_ms = timed_steady(torch, lambda: tt.mp2_energy(B, eo, ev), max(5, args.steps))
+    out["f64_shard_of_8"] = {"max_ms": round(max(shard_ms), 4), "min_ms": round(min(shard_ms), 4),
+                             "sum_ms": round(sum(shard_ms), 4), "whole_ms": round(whole_ms, 4),
+                             "balance": round(min(shard_ms) / max(shard_ms), 4)}
     return out
 
 

@@ -136,6 +136,28 @@ int tt_mp2_energy(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
                   int deterministic, void* stream);
 
 /*
+ * Number of MP2 work units for nocc, nvir: one per occupied pair i <= j and
+ * pair of 64-row virtual blocks p <= q, numbered pair-major
+ * (nocc(nocc+1)/2 * nblk(nblk+1)/2, nblk = ceil(nvir/64)).
+ */
+int64_t tt_mp2_energy_unit_count(int64_t nocc, int64_t nvir);
+
+/*
+ * The part of the MP2 energy that work units [first_unit, first_unit +
+ * n_units) contribute, written to energy_out (one element of dtype); the
+ * units of any partition of [0, tt_mp2_energy_unit_count) sum to the
+ * tt_mp2_energy result (up to the rounding of that final sum). Arguments and
+ * workspace as tt_mp2_energy. No counterpart in the reference: it is the
+ * single-GPU piece of a sharded MP2 (each GPU takes a contiguous range of
+ * units with B replicated, then one scalar all-reduce).
+ */
+int tt_mp2_energy_shard(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
+                        const void* B, const void* eps_occ, const void* eps_vir,
+                        int64_t first_unit, int64_t n_units,
+                        void* energy_out, void* workspace, size_t workspace_bytes,
+                        int deterministic, void* stream);
+
+/*
  * tt_mp2_energy without a workspace, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). No counterpart in the reference. Same arguments,

@@ -18,7 +18,7 @@ HEADER = os.path.join(ROOT, "include", "trntensor_hip.h")
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tt_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(tt_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -175,3 +175,14 @@ def test_plain_c_client_compiles_links_and_runs(tmp_path):
     run = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "c abi ok" in run.stdout
+
+
+def test_mp2_shard_range_checks_need_no_device(lib):
+    assert lib.tt_mp2_energy_unit_count(64, 320) == 2080 * 15
+    assert lib.tt_mp2_energy_unit_count(0, 320) == 0
+    dummy = ctypes.c_void_p(256)
+    ws = lib.tt_mp2_energy_workspace_bytes(1, 4, 70, 16)
+    st = lib.tt_mp2_energy_shard(1, 4, 70, 16, dummy, dummy, dummy, 25, 6, dummy, dummy, ws, 1, None)
+    assert st == _lib.TT_INVALID and b"outside" in lib.tt_last_error()  # 10 pairs x 3 block pairs = 30 units
+    st = lib.tt_mp2_energy_shard(1, 4, 70, 16, dummy, dummy, dummy, -1, 2, dummy, dummy, ws, 1, None)
+    assert st == _lib.TT_INVALID

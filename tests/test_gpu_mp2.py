@@ -115,6 +115,31 @@ def test_mp2_mixed_dtypes_promote(hip, b_dt, e_dt):
     assert float(got) == float(exact)
 
 
+@pytest.mark.parametrize("world", [1, 3, 8])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_mp2_shards_sum_to_whole(hip, world, dtype):
+    """tt_mp2_energy_shard: the contributions of a balanced partition of the
+    work units sum to the whole energy (one shard: bitwise the whole)."""
+    B, eo, ev = (x.cuda() for x in inputs(12, 150, 96, dtype=dtype, seed=13))
+    whole = float(tt.mp2_energy(B, eo, ev))
+    parts = [tt.mp2_energy_shard(B, eo, ev, r, world) for r in range(world)]
+    assert all(p.dtype == dtype and p.shape == () for p in parts)
+    total = sum(float(p) for p in parts)
+    if world == 1:
+        assert float(parts[0]) == whole
+    assert rel(total, whole) <= (1e-13 if dtype == torch.float64 else 1e-6)
+    ref = cpu_ref.mp2_energy(*(x.cpu().double() for x in (B, eo, ev)))
+    assert rel(total, ref) <= (1e-10 if dtype == torch.float64 else 1e-5)
+
+
+def test_mp2_shard_errors(hip):
+    B, eo, ev = (x.cuda() for x in inputs(3, 20, 8, seed=1))
+    with pytest.raises(ValueError, match="rank"):
+        tt.mp2_energy_shard(B, eo, ev, 2, 2)
+    with pytest.raises(ValueError, match="eps_vir"):
+        tt.mp2_energy_shard(B, eo, ev[:5], 0, 2)
+
+
 def test_mp2_cpu_tensors_round_trip(hip):
     """CPU operands are staged through the device; the result comes back on the CPU."""
     B, eo, ev = inputs(4, 40, 24, seed=9)
@@ -182,6 +207,14 @@ def test_mp2_config4_fp32_matches_oracle(hip, config4):
     ref = cpu_ref.mp2_energy(B, eo, ev)
     got = tt.mp2_energy(B.cuda(), eo.cuda(), ev.cuda())
     assert rel(got, ref) <= 1e-5, (float(got), float(ref))
+
+
+def test_mp2_config4_eight_shards(hip, config4):
+    """Config 4 split over eight GPUs' shares (run one after another here)."""
+    B, eo, ev = (x.cuda() for x in config4)
+    whole = float(tt.mp2_energy(B, eo, ev))
+    total = sum(float(tt.mp2_energy_shard(B, eo, ev, r, 8)) for r in range(8))
+    assert rel(total, whole) <= 1e-13
 
 
 def test_mp2_config4_invariants(hip, config4):

@@ -22,7 +22,7 @@ from .plan import (
     plan_cache_info,
     plan_contraction,
 )
-from .quantum import ao_to_mo_transform, mp2_energy
+from .quantum import ao_to_mo_transform, mp2_energy, mp2_energy_shard
 
 __all__ = [
     "einsum",
@@ -41,5 +41,6 @@ __all__ = [
     "to_xla",
     "from_xla",
     "mp2_energy",
+    "mp2_energy_shard",
     "ao_to_mo_transform",
 ]

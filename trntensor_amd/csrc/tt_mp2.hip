@@ -122,7 +122,8 @@ struct Mp2Args {
     int64_t naux;
     int nocc, nvir, nblk;
     int64_t npq;     // nblk * (nblk + 1) / 2
-    int64_t ntasks;  // npq * nocc * (nocc + 1) / 2
+    int64_t first;   // first work unit of this launch
+    int64_t ntasks;  // work units in this launch (of npq * nocc * (nocc + 1) / 2)
 };
 
 // Index of (x, y), x <= y < n, in row-major upper-triangle order -> (x, y).
@@ -182,6 +183,25 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
 #pragma unroll
         for (int b = 0; b < 2; ++b) f1[b] = PN::frag(lds(buf, 1), wc + 16 * b, lane);
         if (NEED_Y) {
+#ifdef TT_MP2_XTHENY
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
+            typename PN::vec_t f2[2], f3[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
+#else
             typename PN::vec_t f2[2], f3[2];
 #pragma unroll
             for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
@@ -196,6 +216,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
                         X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
                         Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
                     }
+#endif
         } else {
 #pragma unroll
             for (int st = 0; st < KS; ++st)
@@ -251,7 +272,11 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
 }
 
 template <typename T, int BK, int AW>
-__global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
+__global__ __launch_bounds__(kMp2Threads)
+#ifdef TT_MP2_WAVES
+__attribute__((amdgpu_waves_per_eu(TT_MP2_WAVES, TT_MP2_WAVES)))
+#endif
+void mp2_energy_kernel(Mp2Args g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
     typedef Panel<T, BK, AW> PN;
@@ -259,7 +284,8 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     __shared__ __attribute__((aligned(16))) T lds[1][4][PN::ELEMS];
     __shared__ double red[4];
 
-    const int64_t task = xcd_remap(blockIdx.x, g.ntasks);
+    const int64_t local = xcd_remap(blockIdx.x, g.ntasks);
+    const int64_t task = g.first + local;
     const int64_t pair = task / g.npq;
     const int64_t u = task - pair * g.npq;
     int i, j, p, q;
@@ -371,7 +397,7 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     double blk = block256_sum(sum, red);
     if (threadIdx.x == 0) {
         if (i != j) blk *= 2.0;
-        if (g.partial) g.partial[task] = blk;
+        if (g.partial) g.partial[local] = blk;
         else atomicAdd(g.accum, blk);
     }
 }
@@ -406,7 +432,7 @@ static int64_t mp2_ntasks(int64_t nocc, int64_t nvir) {
 
 template <typename T>
 static int mp2_typed(int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eo, const void* ev,
-                     void* out, void* ws, int det, hipStream_t st) {
+                     void* out, void* ws, int det, hipStream_t st, int64_t first, int64_t count) {
     Mp2Args g;
     g.B = B;
     g.eo = eo;
@@ -416,7 +442,8 @@ static int mp2_typed(int64_t nocc, int64_t nvir, int64_t naux, const void* B, co
     g.nvir = (int)nvir;
     g.nblk = (int)((nvir + kMp2Tile - 1) / kMp2Tile);
     g.npq = (int64_t)g.nblk * (g.nblk + 1) / 2;
-    g.ntasks = mp2_ntasks(nocc, nvir);
+    g.first = first;
+    g.ntasks = count;
     double* w = static_cast<double*>(ws);
     if (det) {
         g.partial = w;
@@ -475,9 +502,11 @@ static int mp2_check(const char* what, int dtype, int64_t nocc, int64_t nvir, in
 }
 
 static int mp2_dispatch(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B, const void* eo,
-                        const void* ev, void* out, void* ws, int det, hipStream_t st) {
-    if (dtype == TT_F64) return mp2_typed<double>(nocc, nvir, naux, B, eo, ev, out, ws, det, st);
-    return mp2_typed<float>(nocc, nvir, naux, B, eo, ev, out, ws, det, st);
+                        const void* ev, void* out, void* ws, int det, hipStream_t st, int64_t first = 0,
+                        int64_t count = -1) {
+    if (count < 0) count = mp2_ntasks(nocc, nvir);
+    if (dtype == TT_F64) return mp2_typed<double>(nocc, nvir, naux, B, eo, ev, out, ws, det, st, first, count);
+    return mp2_typed<float>(nocc, nvir, naux, B, eo, ev, out, ws, det, st, first, count);
 }
 
 // Scratch of the allocation-free entry point: the per-workgroup partials
@@ -547,4 +576,27 @@ extern "C" int tt_mp2_energy_noalloc(int dtype, int64_t nocc, int64_t nvir, int6
     if (rc != TT_OK) return rc;
     return mp2_dispatch(dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, ws, deterministic,
                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t tt_mp2_energy_unit_count(int64_t nocc, int64_t nvir) {
+    if (nocc < 0 || nvir < 0) return 0;
+    return tt::mp2_ntasks(nocc, nvir);
+}
+
+extern "C" int tt_mp2_energy_shard(int dtype, int64_t nocc, int64_t nvir, int64_t naux, const void* B,
+                                   const void* eps_occ, const void* eps_vir, int64_t first_unit, int64_t n_units,
+                                   void* energy_out, void* workspace, size_t workspace_bytes, int deterministic,
+                                   void* stream) {
+    using namespace tt;
+    int rc = mp2_check("tt_mp2_energy_shard", dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out);
+    if (rc != TT_OK) return rc;
+    const int64_t total = mp2_ntasks(nocc, nvir);
+    if (first_unit < 0 || n_units < 0 || first_unit > total || n_units > total - first_unit)
+        return set_error(TT_INVALID, "tt_mp2_energy_shard: units [%lld, %lld) outside [0, %lld)", (long long)first_unit,
+                         (long long)(first_unit + n_units), (long long)total);
+    const size_t need = tt_mp2_energy_workspace_bytes(dtype, nocc, nvir, naux);
+    if (!workspace || workspace_bytes < need)
+        return set_error(TT_INVALID, "tt_mp2_energy_shard: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    return mp2_dispatch(dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, workspace, deterministic,
+                        static_cast<hipStream_t>(stream), first_unit, n_units);
 }

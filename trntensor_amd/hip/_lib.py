@@ -44,6 +44,8 @@ SIGNATURES = {
     "tt_mp2_energy_workspace_bytes": (_sz, [_int, _i64, _i64, _i64]),
     "tt_mp2_energy": (_int, [_int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _int, _vp]),
     "tt_mp2_energy_noalloc": (_int, [_int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _int, _vp]),
+    "tt_mp2_energy_unit_count": (_i64, [_i64, _i64]),
+    "tt_mp2_energy_shard": (_int, [_int, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _int, _vp]),
     "tt_ao_to_mo_workspace_bytes": (_sz, [_int, _i64, _i64, _i64, _i64]),
     "tt_ao_to_mo_transform": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tt_mfma_rate_probe": (_int, [_int, _i64, _i64, _vp, _vp]),

@@ -233,6 +233,36 @@ def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     return e.to(res_dtype).to(orig)
 
 
+def _hip_mp2_energy_shard(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, rank: int, world_size: int,
+                          deterministic: bool = True) -> torch.Tensor:
+    """Contribution of shard `rank` of `world_size` (a contiguous, balanced
+    range of work units, tt_mp2_energy_shard) to the MP2 energy; the shards'
+    values sum to the whole energy. 0-D tensor in the promoted dtype on B's
+    device."""
+    require_hip()
+    if not 0 <= rank < world_size:
+        raise ValueError(f"rank {rank} outside world_size {world_size}")
+    lib = _lib.load()
+    (b, eo, ev), orig = place(B, eps_occ, eps_vir)
+    res_dtype = torch.promote_types(torch.promote_types(b.dtype, eo.dtype), ev.dtype)
+    cd = compute_dtype(res_dtype)
+    b, eo, ev = (x.to(cd).contiguous() for x in (b, eo, ev))
+    nocc, nvir, naux = b.shape
+    total = lib.tt_mp2_energy_unit_count(nocc, nvir)
+    first = total * rank // world_size
+    count = total * (rank + 1) // world_size - first
+    code = engine.dtype_code(cd)
+    wsb = lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux)
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=b.device)
+    e = torch.empty((), dtype=cd, device=b.device)
+    st = lib.tt_mp2_energy_shard(
+        code, nocc, nvir, naux, engine._ptr(b), engine._ptr(eo), engine._ptr(ev), first, count,
+        engine._ptr(e), engine._ptr(ws), wsb, int(bool(deterministic)), engine._stream_ptr(b.device),
+    )
+    _lib.check(st, "tt_mp2_energy_shard")
+    return e.to(res_dtype).to(orig)
+
+
 def _hip_ao_to_mo_transform(eri: torch.Tensor, C_occ: torch.Tensor, C_vir: torch.Tensor) -> torch.Tensor:
     """Full AO->MO transform on tt_ao_to_mo_transform (reference
     _nki_ao_to_mo_transform, dispatch.py:286-336). Result on eri's device."""

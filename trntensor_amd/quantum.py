@@ -38,6 +38,32 @@ def mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor) ->
     return dispatch._hip_mp2_energy(B, eps_occ, eps_vir)
 
 
+def mp2_energy_shard(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, rank: int,
+                     world_size: int) -> torch.Tensor:
+    """One GPU's share of :func:`mp2_energy` for a run sharded over
+    ``world_size`` GPUs (no counterpart in the reference).
+
+    The energy is a sum over independent work units (occupied pair i <= j,
+    pair of 64-row virtual blocks); shard ``rank`` takes a contiguous,
+    balanced range of them. With B and the orbital energies on every GPU,
+    ``torch.distributed.all_reduce`` of the shards' values (one scalar)
+    gives the energy::
+
+        e = trntensor.mp2_energy_shard(B, eo, ev, rank, world_size)
+        torch.distributed.all_reduce(e)        # e == mp2_energy(B, eo, ev)
+
+    Same validation and dtype as :func:`mp2_energy`.
+    """
+    if B.dim() != 3:
+        raise ValueError(f"B must be 3D (nocc, nvir, naux); got shape {tuple(B.shape)}")
+    nocc, nvir, _naux = B.shape
+    if eps_occ.shape != (nocc,):
+        raise ValueError(f"eps_occ must have shape ({nocc},); got {tuple(eps_occ.shape)}")
+    if eps_vir.shape != (nvir,):
+        raise ValueError(f"eps_vir must have shape ({nvir},); got {tuple(eps_vir.shape)}")
+    return dispatch._hip_mp2_energy_shard(B, eps_occ, eps_vir, rank, world_size)
+
+
 def ao_to_mo_transform(eri: torch.Tensor, C_occ: torch.Tensor, C_vir: torch.Tensor) -> torch.Tensor:
     """Four-index AO->MO transform of density-fitted integrals.
 
