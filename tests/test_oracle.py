@@ -330,3 +330,21 @@ def test_integer_einsum_wraps_like_int64_truncated():
         assert got.dtype == dt
         assert np.array_equal(got.to(torch.int64).numpy(), want)
         assert np.abs(wide).max() >= (1 << (bits - 1)), "the data must overflow the narrow type"
+
+
+@pytest.mark.parametrize("sub,shapes", [("ij,jk->ik", [(7, 9), (9, 5)]), ("bij,bjk->bik", [(2, 4, 6), (2, 6, 3)]),
+                                        ("ij,jk,kl->il", [(3, 4), (4, 5), (5, 2)]), ("ii->", [(6, 6)]),
+                                        ("mi,mnP->inP", [(5, 2), (5, 5, 3)])])
+def test_complex_einsum_matches_numpy(sub, shapes):
+    """The oracle's complex contractions (torch on the CPU) against numpy's
+    complex128 einsum, an independent implementation, plus a complex alpha
+    and beta with a real out (promotion to complex)."""
+    g = np.random.default_rng(len(sub))
+    ops = [g.standard_normal(s) + 1j * g.standard_normal(s) for s in shapes]
+    got = cpu_ref.einsum(sub, *[torch.from_numpy(o) for o in ops])
+    want = np.einsum(sub, *ops)
+    assert got.dtype == torch.complex128
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+    out = g.standard_normal(np.shape(want))
+    got = cpu_ref.einsum(sub, *[torch.from_numpy(o) for o in ops], alpha=1 - 2j, beta=0.5j, out=torch.from_numpy(out))
+    np.testing.assert_allclose(got.numpy(), (1 - 2j) * want + 0.5j * out, rtol=1e-12, atol=1e-12)
