@@ -183,25 +183,6 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
 #pragma unroll
         for (int b = 0; b < 2; ++b) f1[b] = PN::frag(lds(buf, 1), wc + 16 * b, lane);
         if (NEED_Y) {
-#ifdef TT_MP2_XTHENY
-#pragma unroll
-            for (int st = 0; st < KS; ++st)
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
-            typename PN::vec_t f2[2], f3[2];
-#pragma unroll
-            for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
-#pragma unroll
-            for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
-#pragma unroll
-            for (int st = 0; st < KS; ++st)
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
-#else
             typename PN::vec_t f2[2], f3[2];
 #pragma unroll
             for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
@@ -216,7 +197,6 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
                         X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
                         Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
                     }
-#endif
         } else {
 #pragma unroll
             for (int st = 0; st < KS; ++st)
@@ -272,11 +252,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
 }
 
 template <typename T, int BK, int AW>
-__global__ __launch_bounds__(kMp2Threads)
-#ifdef TT_MP2_WAVES
-__attribute__((amdgpu_waves_per_eu(TT_MP2_WAVES, TT_MP2_WAVES)))
-#endif
-void mp2_energy_kernel(Mp2Args g) {
+__global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
     typedef Panel<T, BK, AW> PN;
