@@ -560,6 +560,33 @@ def bench_c1(torch, tt, dev, args):
     t_loop = per_call(loop, 10)
     t_fused = per_call(lambda: float(tt.mp2_energy(B, eo, ev)), 50)
     res = {"einsum_loop_ms": round(t_loop * 1e3, 3), "fused_cpu_operands_ms": round(t_fused * 1e3, 3)}
+    # The loop's 64 contractions on device-resident operands: eager calls, and
+    # the same calls recorded once in a HIP graph and replayed (launch-bound
+    # loops are what graphs are for; the library allocates nothing and issues
+    # no memsets, so its launches record as plain kernel nodes).
+    Bd = B.to(dev)
+
+    def dev_loop():
+        return [tt.einsum("ap,bp->ab", Bd[i], Bd[j]) for i in range(8) for j in range(8)]
+
+    def synced(fn):
+        def run():
+            fn()
+            torch.cuda.synchronize()
+        return run
+
+    t_dev = per_call(synced(dev_loop), 20)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dev_loop()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dev_loop()
+    t_graph = per_call(synced(graph.replay), 50)
+    res["device_einsum_loop_ms"] = round(t_dev * 1e3, 3)
+    res["device_einsum_loop_graph_replay_ms"] = round(t_graph * 1e3, 3)
     if not args.no_cpu:
         from oracle import cpu_ref
 
