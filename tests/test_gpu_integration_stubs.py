@@ -1,5 +1,5 @@
-"""The reference-side ctypes stubs written out in INTEGRATION.md (section 4)
-run as documented: the python block is executed with the library path
+"""The reference-side ctypes stubs of the integration guide run as written:
+the guide's python block that defines them is executed with the library path
 pointed at the in-tree build, and each stub is checked against the oracle."""
 
 import os
