@@ -110,7 +110,14 @@ int tt_gemm_dot(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Workspace (device bytes) that tt_mp2_energy needs for this problem.
+ * Workspace (device bytes) for tt_mp2_energy and tt_mp2_energy_shard: one
+ * double per work unit plus one, and, when naux is not a multiple of 16, a
+ * copy of B with each row padded with zeros to the next multiple of 16
+ * elements (nocc * nvir * that many elements of dtype). Both calls accept any
+ * workspace that holds the partials (this function's value for naux rounded
+ * up to a multiple of 16); they make the padded copy, and then run at the
+ * rate of an aligned naux, only when the workspace holds it too and starts
+ * on a 256-byte boundary. The energy is the same, bitwise, either way.
  */
 size_t tt_mp2_energy_workspace_bytes(int dtype, int64_t nocc, int64_t nvir, int64_t naux);
 

@@ -71,6 +71,25 @@ def test_mp2_workspace_and_errors(lib):
     assert st == _lib.TT_UNSUPPORTED
 
 
+def test_mp2_workspace_holds_a_row_padded_copy_for_unaligned_naux(lib):
+    part = (((2080 * 15 + 1) * 8 + 255) // 256) * 256
+    for code, elem in ((1, 8), (0, 4)):
+        # naux a multiple of 16: the partials only
+        assert lib.tt_mp2_energy_workspace_bytes(code, 64, 320, 1200) == part
+        assert lib.tt_mp2_energy_workspace_bytes(code, 64, 320, 1216) == part
+        # otherwise also B with rows padded to the next multiple of 16
+        for naux, pitch in ((1199, 1200), (1190, 1200), (1201, 1216), (1, 16)):
+            pad = (64 * 320 * pitch * elem + 255) // 256 * 256
+            assert lib.tt_mp2_energy_workspace_bytes(code, 64, 320, naux) == part + pad
+    assert lib.tt_mp2_energy_workspace_bytes(1, 0, 320, 1199) == 256
+    # Both entry points accept the partials' size for any naux: below it they refuse.
+    dummy = ctypes.c_void_p(256)
+    st = lib.tt_mp2_energy(1, 64, 320, 1199, dummy, dummy, dummy, dummy, dummy, part - 8, 1, None)
+    assert st == _lib.TT_INVALID and f"need {part}".encode() in lib.tt_last_error()
+    st = lib.tt_mp2_energy_shard(1, 64, 320, 1199, dummy, dummy, dummy, 0, 1, dummy, dummy, part - 8, 1, None)
+    assert st == _lib.TT_INVALID and f"need {part}".encode() in lib.tt_last_error()
+
+
 def test_ao2mo_and_strided_errors(lib):
     dummy = ctypes.c_void_p(256)
     assert lib.tt_ao_to_mo_workspace_bytes(1, 512, 64, 320, 1536) >= 64 * 512 * 1536 * 8

@@ -82,6 +82,50 @@ def test_mp2_unaligned_naux_matches_oracle(hip, shape, dtype):
     assert rel(got, ref) <= (1e-10 if dtype == torch.float64 else 1e-5), (float(got), float(ref))
 
 
+PADDED = [(4, 70, 1199), (6, 130, 1190), (3, 64, 37), (2, 65, 1), (5, 64, 200), (3, 100, 15)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("shape", PADDED)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_mp2_row_padded_copy_is_bitwise_neutral(hip, shape, dtype, offset):
+    """naux not a multiple of 16: with the full workspace tt_mp2_energy runs
+    on a row-padded copy of B; with only the partials' room (the query for
+    naux rounded up to 16), or with the full size but a workspace off a
+    256-byte boundary, it runs on B as given. All three give one energy,
+    bitwise, within the bar of the oracle. offset=1 starts B one element past
+    an aligned address, so the copy reads unaligned rows."""
+    from trntensor_amd.hip import _lib, engine
+
+    lib = _lib.load()
+    nocc, nvir, naux = shape
+    B, eo, ev = inputs(nocc, nvir, naux, dtype=dtype, seed=sum(shape) + offset)
+    print(f"padded copy {dtype} {shape} offset {offset}", flush=True)
+    buf = torch.zeros(B.numel() + offset, dtype=dtype, device="cuda")
+    buf[offset:] = B.reshape(-1).cuda()
+    b = buf[offset:].view(nocc, nvir, naux)
+    o, v = eo.cuda(), ev.cuda()
+    code = engine.dtype_code(dtype)
+    full = int(lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux))
+    part = int(lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, (naux + 15) // 16 * 16))
+    pitch = (naux + 15) // 16 * 16
+    assert full - part == (nocc * nvir * pitch * B.element_size() + 255) // 256 * 256
+    arena = torch.empty(full + 256, dtype=torch.uint8, device="cuda")
+    assert arena.data_ptr() % 256 == 0
+    stream = engine._stream_ptr(b.device)
+    vals = []
+    for ws_ptr, ws_bytes in ((arena.data_ptr(), full), (arena.data_ptr(), part), (arena.data_ptr() + 8, full)):
+        e = torch.full((), float("nan"), dtype=dtype, device="cuda")
+        st = lib.tt_mp2_energy(code, nocc, nvir, naux, b.data_ptr(), o.data_ptr(), v.data_ptr(), e.data_ptr(),
+                               ws_ptr, ws_bytes, 1, stream)
+        _lib.check(st, "tt_mp2_energy")
+        torch.cuda.synchronize()
+        vals.append(float(e.cpu()))
+    assert vals[0] == vals[1] == vals[2], vals
+    got = torch.tensor(vals[0], dtype=torch.float64)
+    assert rel(got, cpu_ref.mp2_energy(B, eo, ev)) <= (1e-10 if dtype == torch.float64 else 1e-5), vals[0]
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_mp2_misaligned_base_pointer(hip, dtype):
     """B contiguous but starting one element past a 16-byte boundary (a view

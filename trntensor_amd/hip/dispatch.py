@@ -252,7 +252,10 @@ def _hip_mp2_energy_shard(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch
     first = total * rank // world_size
     count = total * (rank + 1) // world_size - first
     code = engine.dtype_code(cd)
-    wsb = lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux)
+    # The partials only (the size for naux rounded up to a multiple of 16):
+    # a shard makes no row-padded copy of B, which would cost each shard's
+    # call as much as it saves on that shard's share of the work.
+    wsb = lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, (naux + 15) // 16 * 16)
     ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=b.device)
     e = torch.empty((), dtype=cd, device=b.device)
     st = lib.tt_mp2_energy_shard(
