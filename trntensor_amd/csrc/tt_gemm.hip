@@ -263,24 +263,66 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         const T* E1 = static_cast<const T*>(g.E1) + bat * g.e1s[4];
         const T* E2 = g.E2 ? static_cast<const T*>(g.E2) + bat * g.e2s[4] : nullptr;
         double sum = 0.0;
+        if constexpr (NBUF == 2) {
+            // Each 16x16 block's eight E loads (branch-free: rows and columns
+            // outside the matrix read element (0, 0)) go out together before
+            // its sums, which keep the order below. Loaded under the
+            // per-element bounds branches, every load waited out a full
+            // latency before its sum: 128 waits per lane at 128 x 128, and
+            // config 5's greedy path took 69.4 ms against 68.4 ms this way
+            // (results bitwise equal). The single-buffer small-M tile keeps
+            // the form below: the batches would cost it a wave per SIMD.
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int64_t col = n0 + wn0 + 16 * j + col_l;
-            const uint32_t nh = fdiv((uint32_t)col, g.ndiv);
-            const uint32_t nl = (uint32_t)col - nh * g.ndiv.d;
-            const int64_t o1n = nh * g.e1s[2] + nl * g.e1s[3];
-            const int64_t o2n = nh * g.e2s[2] + nl * g.e2s[3];
+            for (int j = 0; j < FN; ++j) {
+                const int64_t col = n0 + wn0 + 16 * j + col_l;
+                const bool cok = col < g.N;
+                const uint32_t nh = fdiv((uint32_t)(cok ? col : 0), g.ndiv);
+                const uint32_t nl = (uint32_t)(cok ? col : 0) - nh * g.ndiv.d;
+                const int64_t o1n = nh * g.e1s[2] + nl * g.e1s[3];
+                const int64_t o2n = nh * g.e2s[2] + nl * g.e2s[3];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
+                for (int i = 0; i < FM; ++i) {
+                    T e1v[4], e2v[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
-                    if (row < g.M && col < g.N) {
-                        const uint32_t mh = fdiv((uint32_t)row, g.mdiv);
-                        const uint32_t ml = (uint32_t)row - mh * g.mdiv.d;
-                        T e = E1[mh * g.e1s[0] + ml * g.e1s[1] + o1n];
-                        if (E2) e = e * E2[mh * g.e2s[0] + ml * g.e2s[1] + o2n];
-                        sum += (double)(acc[i][j][r] * e);
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
+                        const bool ok = cok && row < g.M;
+                        const uint32_t mh = fdiv((uint32_t)(ok ? row : 0), g.mdiv);
+                        const uint32_t ml = (uint32_t)(ok ? row : 0) - mh * g.mdiv.d;
+                        e1v[r] = E1[ok ? mh * g.e1s[0] + ml * g.e1s[1] + o1n : 0];
+                        if (E2) e2v[r] = E2[ok ? mh * g.e2s[0] + ml * g.e2s[1] + o2n : 0];
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
+                        if (cok && row < g.M) {
+                            T e = e1v[r];
+                            if (E2) e = e * e2v[r];
+                            sum += (double)(acc[i][j][r] * e);
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int64_t col = n0 + wn0 + 16 * j + col_l;
+                const uint32_t nh = fdiv((uint32_t)col, g.ndiv);
+                const uint32_t nl = (uint32_t)col - nh * g.ndiv.d;
+                const int64_t o1n = nh * g.e1s[2] + nl * g.e1s[3];
+                const int64_t o2n = nh * g.e2s[2] + nl * g.e2s[3];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + wm0 + 16 * i + MF::row(lgrp, r);
+                        if (row < g.M && col < g.N) {
+                            const uint32_t mh = fdiv((uint32_t)row, g.mdiv);
+                            const uint32_t ml = (uint32_t)row - mh * g.mdiv.d;
+                            T e = E1[mh * g.e1s[0] + ml * g.e1s[1] + o1n];
+                            if (E2) e = e * E2[mh * g.e2s[0] + ml * g.e2s[1] + o2n];
+                            sum += (double)(acc[i][j][r] * e);
+                        }
                     }
                 }
             }
