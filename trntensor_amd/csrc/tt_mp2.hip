@@ -183,6 +183,32 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
 #pragma unroll
         for (int b = 0; b < 2; ++b) f1[b] = PN::frag(lds(buf, 1), wc + 16 * b, lane);
         if (NEED_Y) {
+            // fp32: X's fragments and MFMAs, then Y's. Holding half a
+            // stage's fragments brings the kernel from 112 to 96 VGPRs, five
+            // workgroups per CU instead of four: 4.16 against 4.21 ms at
+            // config 4, energies bitwise equal (each accumulator's MFMAs keep
+            // their order). fp64 stays at three workgroups either way (150
+            // VGPRs; the LDS would hold four) and measured no gain.
+            if (sizeof(T) == 4) {
+#pragma unroll
+                for (int st = 0; st < KS; ++st)
+#pragma unroll
+                    for (int a = 0; a < 2; ++a)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
+                typename PN::vec_t f2[2], f3[2];
+#pragma unroll
+                for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
+#pragma unroll
+                for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
+#pragma unroll
+                for (int st = 0; st < KS; ++st)
+#pragma unroll
+                    for (int a = 0; a < 2; ++a)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
+                return;
+            }
             typename PN::vec_t f2[2], f3[2];
 #pragma unroll
             for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
