@@ -35,7 +35,7 @@ constexpr int kThreads = 256;
 //       contiguous bytes of the k-row (coalesced loads, conflict-free stores).
 // RC k-rows are padded by 4 elements: the four lane groups of a fragment read
 // (k-rows 4 g + s) then land on disjoint LDS banks.
-template <typename T, int ROWS, bool KC, bool VEC, int BK>
+template <typename T, int ROWS, bool KC, bool VEC, int BK, bool NT = false>
 struct Stage {
     static constexpr int V = Vec16<T>::n;
     static constexpr int E = ROWS * BK / kThreads;
@@ -79,8 +79,10 @@ struct Stage {
         if (FAST) {
             const T* src = KC ? p + (row0 + r) * ld + (k0 + k) : p + (k0 + k) * ld + (row0 + r);
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
-                reg[c] = *reinterpret_cast<const vec_t*>(KC ? src + pk(c) : src + pk(c) * ld + prow(c));
+            for (int c = 0; c < NC; ++c) {
+                const vec_t* q = reinterpret_cast<const vec_t*>(KC ? src + pk(c) : src + pk(c) * ld + prow(c));
+                reg[c] = NT ? __builtin_nontemporal_load(q) : *q;
+            }
         } else {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
@@ -140,7 +142,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     typedef typename MF::acc_t acc_t;
     // A rows are m: k-contiguous unless transposed. B rows are n: k-contiguous iff transposed.
     typedef Stage<T, BM, !TA, VEC, BK> SA;
-    typedef Stage<T, BN, TB, VEC, BK> SB;
+    // The single-buffer small-M tile reads B once (one tile row; the launcher
+    // sends a batch-broadcast B elsewhere), so B's loads are non-temporal and
+    // leave the L2 to A, which every workgroup re-reads: AO->MO half
+    // transform 0.909-0.920 -> 0.899-0.900 ms, results bitwise equal.
+    // Non-temporal loads of A as well, or on tiles that re-read B, cost 7-18%.
+    typedef Stage<T, BN, TB, VEC, BK, NBUF == 1 && PRIO> SB;
     // Each wavefront owns an (16 FM) x (16 FN) sub-tile: FM x FN MFMA blocks.
     constexpr int WM = 16 * FM, WN = 16 * FN;
     constexpr int WAVES_N = BN / WN;
@@ -416,8 +423,11 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // priority for the burst. Same box, results bitwise equal: 64 x 786432 x
     // 512 0.928-0.952 -> 0.895-0.927 ms (+2-3%). Raised priority measured
     // slower for the batched and large fp64 tiles (64 x 512^3: +12% time), so
-    // it stays on this tile only.
-    if (sizeof(T) == 8 && !DOT && g.M <= 64) return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
+    // it stays on this tile only. This tile streams B (non-temporal loads), so
+    // a B broadcast over the batch (stride 0, re-read per batch entry) takes
+    // the two-buffer tile below.
+    if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
+        return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
         return launch_tile<T, 64, 128, 2, 4, DOT>(g, ta, tb, vec, st);
     if (g.N <= 64) return launch_tile<T, 256, 64, 4, 4, DOT>(g, ta, tb, vec, st);
