@@ -133,6 +133,25 @@ class TestPlanCache:
     def setup_method(self):
         trntensor.clear_plan_cache()
 
+    def test_errors_around_a_cached_plan(self):
+        """Validation runs on cache misses only; a call that would fail never
+        matches a cached key (same subscripts and shapes), so every error
+        still surfaces, in the reference's precedence."""
+        A, B = t(4, 3), t(3, 5)
+        trntensor.plan_contraction("ij,jk->ik", A, B)
+        with pytest.raises(ValueError, match="index 'j'"):
+            trntensor.plan_contraction("ij,jk->ik", A, t(5, 6))
+        with pytest.raises(ValueError, match="2 operand term"):
+            trntensor.plan_contraction("ij,jk->ik", A, B, t(5, 2))
+        with pytest.raises(ValueError, match="precision must be"):
+            trntensor.plan_contraction("ij,jk->ik", A, B, precision="super")
+        with pytest.raises(ValueError, match="optimize must be"):
+            trntensor.plan_contraction("ij,jk->ik", A, B, optimize="fastest")
+        # subscript errors take precedence over a bad keyword
+        with pytest.raises(ValueError, match="index 'j'"):
+            trntensor.plan_contraction("ij,jk->ik", A, t(5, 6), precision="super")
+        assert trntensor.plan_cache_info()["size"] == 1
+
     def test_hit_miss_clear_and_precision_key(self):
         A, B = t(4, 3), t(3, 5)
         p1 = trntensor.plan_contraction("ij,jk->ik", A, B)

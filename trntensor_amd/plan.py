@@ -140,8 +140,12 @@ def plan_contraction(
 ) -> ContractionPlan:
     """Validate, then return the (cached) plan for this subscript/shape/precision.
 
-    Validation runs on every call, before the cache lookup; an unknown
-    ``precision`` raises ``ValueError``. Two operands get a binary strategy,
+    An unknown ``precision`` or ``optimize`` raises ``ValueError`` on every
+    call. The subscripts are validated against the operands when the plan is
+    not cached: the outcome depends only on the subscripts and the operand
+    shapes, which the cache key holds, so a cached plan means an identical
+    call already passed (the reference validates before its lookup; the
+    errors raised are the same). Two operands get a binary strategy,
     three or more a path, one operand the "torch" label
     (reference trntensor/plan.py:140-185).
 
@@ -151,15 +155,16 @@ def plan_contraction(
     the same per-step cost (see ``_optimal_path_search``). It changes only the
     order of pairwise steps, never the result beyond rounding.
     """
-    _validate_subscripts(subscripts, operands)
-    if precision not in ("fast", "kahan", "dd"):
-        raise ValueError(f"precision must be 'fast', 'kahan', or 'dd', got {precision!r}")
-    if optimize not in PATH_SEARCHES:
+    if precision not in ("fast", "kahan", "dd") or optimize not in PATH_SEARCHES:
+        _validate_subscripts(subscripts, operands)  # its errors come first, as in the reference
+        if precision not in ("fast", "kahan", "dd"):
+            raise ValueError(f"precision must be 'fast', 'kahan', or 'dd', got {precision!r}")
         raise ValueError(f"optimize must be one of {PATH_SEARCHES}, got {optimize!r}")
     key = _shape_key(subscripts, operands, precision, optimize)
     hit = _PLAN_CACHE.get(key)
     if hit is not None:
         return hit
+    _validate_subscripts(subscripts, operands)
 
     lhs, out = _parse_subscripts(subscripts)
     terms = lhs.split(",")
