@@ -87,6 +87,81 @@ class TestMisplannedPatterns:
         close(got, ref)
 
 
+class TestRandomFrontEnd:
+    """Random calls of the public einsum: one to three operands, letters
+    repeated within a term (diagonals) and across terms, implicit and
+    explicit outputs, extents 1-6, fp32 and fp64, non-contiguous views and
+    CPU operands, alpha/beta with an `out` of the result's shape in the same
+    or a wider dtype. Expected value: alpha * numpy's float64 einsum + beta *
+    out (an implementation independent of the oracle's torch calls, so the
+    patterns the reference's matmul/bmm executors mishandle are covered
+    too). Bar per element: the recursive-summation bound
+    gamma_(n+3) * (|alpha| einsum(|ops|) + |beta out|) for n terms per
+    output, doubled per pairwise step of a path, plus one rounding of the
+    result to its dtype; dtype and shape as result.add(out, alpha=beta)
+    (trntensor/einsum.py:99-102)."""
+
+    @staticmethod
+    def _operand(rng, gen, shape, dt, on_cpu):
+        x = torch.randn(*shape, generator=gen, dtype=torch.float64).to(dt)
+        if len(shape) >= 2 and rng.random() < 0.3:
+            perm = list(range(len(shape)))
+            rng.shuffle(perm)
+            inv = [perm.index(k) for k in range(len(shape))]
+            x = x.permute(*perm).contiguous().permute(*inv)  # same values, non-contiguous strides
+        return x if on_cpu else x.cuda()
+
+    @pytest.mark.parametrize(
+        "ncases,letters,lo,hi,seed",
+        [(200, "abcde", 1, 6, 2024), (60, "abcd", 6, 40, 7)],
+        ids=["small-extents", "gemm-sized"],
+    )
+    def test_random_calls(self, hip, ncases, letters, lo, hi, seed):
+        import random
+
+        rng = random.Random(seed)
+        gen = torch.Generator().manual_seed(seed)
+        for case in range(ncases):
+            ext = {c: rng.randint(lo, hi) for c in letters}
+            nops = rng.choice([1, 2, 2, 2, 3, 3])
+            terms = ["".join(rng.choice(letters) for _ in range(rng.randint(1, 3))) for _ in range(nops)]
+            seen = sorted(set("".join(terms)))
+            if rng.random() < 0.2:
+                sub = ",".join(terms)
+            else:
+                out_letters = "".join(c for c in rng.sample(seen, len(seen)) if rng.random() < 0.5)
+                sub = ",".join(terms) + "->" + out_letters
+            dt = rng.choice([torch.float32, torch.float64])
+            on_cpu = rng.random() < 0.15  # CPU operands are staged through the GPU
+            ops = [self._operand(rng, gen, [ext[c] for c in t], dt, on_cpu) for t in terms]
+            ref = brute.einsum_f64(sub, *[o.cpu().numpy() for o in ops])
+            scale = np.abs(brute.einsum_f64(sub, *[np.abs(o.cpu().numpy()) for o in ops]))
+            kw = {}
+            res_dt = dt
+            out_part = np.zeros_like(ref)
+            alpha = 1.0
+            if rng.random() < 0.4:
+                alpha = rng.choice([0.5, -1.25, 2.0])
+                beta = rng.choice([0.0, 0.75, -0.5])
+                out_dt = dt if rng.random() < 0.7 else torch.float64
+                out = torch.randn(tuple(np.shape(ref)), generator=gen, dtype=torch.float64).to(out_dt)
+                kw = dict(alpha=alpha, beta=beta, out=out.cuda() if ops[0].is_cuda else out)
+                res_dt = torch.promote_types(dt, out_dt)
+                out_part = beta * out.double().numpy()
+            print(f"random case {case}: {sub} {dt} {kw.get('alpha', 1.0)} {kw.get('beta', 0.0)}", flush=True)
+            got = trntensor.einsum(sub, *ops, **kw)
+            assert got.dtype == res_dt and tuple(got.shape) == tuple(np.shape(ref)), (sub, got.dtype, got.shape)
+            want = alpha * ref + out_part
+            out_str = cpu_ref.parse_subscripts(sub)[1]
+            n_terms = int(np.prod([ext[c] for c in set("".join(terms)) if c not in out_str]))
+            u = 2.0**-53 if dt == torch.float64 else 2.0**-24
+            steps = max(1, nops - 1)
+            bar = 2**steps * (n_terms + 3) * u / (1 - (n_terms + 3) * u) * (abs(alpha) * scale + np.abs(out_part))
+            bar = bar + (2.0**-53 if res_dt == torch.float64 else 2.0**-24) * np.abs(want) + 1e-300
+            err = np.abs(got.cpu().double().numpy() - want)
+            assert np.all(err <= bar), (case, sub, dt, float(np.max(err / bar)))
+
+
 class TestMultiEinsum:
     """tests/test_einsum.py:87-150."""
 
