@@ -171,27 +171,6 @@ def compute_dtype(dt: torch.dtype) -> torch.dtype:
 # ---------------------------------------------------------------------------
 # entry points replacing the reference's NKI dispatchers
 # ---------------------------------------------------------------------------
-def hip_matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    """2-D ``A @ B`` on the MFMA GEMM core (reference nki_matmul, dispatch.py:187-237)."""
-    return _binary("ij,jk->ik", A, B)
-
-
-def hip_batched_matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    """``A[b] @ B[b]`` on the MFMA GEMM core (reference nki_batched_matmul, dispatch.py:339-387)."""
-    return _binary("bij,bjk->bik", A, B)
-
-
-def _binary(sub: str, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    require_hip()
-    lhs, out = sub.split("->")
-    (a, b), orig = place(A, B)
-    if a.dtype != b.dtype:
-        raise RuntimeError(f"expected both operands to have the same dtype, got {a.dtype} and {b.dtype}")
-    cd = compute_dtype(a.dtype)
-    res = engine.contract(lhs.split(","), out, [a.to(cd), b.to(cd)], prefer_gemm=True)
-    return res.to(a.dtype).to(orig)
-
-
 def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
     """Fused DF-MP2 energy on tt_mp2_energy (reference _nki_mp2_energy, dispatch.py:240-283).
 
