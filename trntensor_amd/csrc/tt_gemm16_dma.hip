@@ -45,11 +45,8 @@ typedef float df32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short du16x8 __attribute__((ext_vector_type(8)));
 typedef short ds16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kDT = 256;                  // workgroup tile rows and columns
 constexpr int kDK = 32;                   // k per stage
 constexpr int kSlots = 4;                 // LDS ring slots (three stages in flight)
-constexpr int kOpBytes = kDT * kDK * 2;   // one operand's stage: 16 KB
-constexpr int kSlotBytes = 2 * kOpBytes;  // A, then B
 
 template <typename T>
 __device__ __forceinline__ df32x4 mma16(du16x8 a, du16x8 b, df32x4 c) {
