@@ -122,6 +122,40 @@ def measured_peaks(torch, dev):
     return out
 
 
+def add_measured_fractions(extra, peaks):
+    """Next to each datasheet fraction in the config results, the same achieved
+    rate over the peak this device sustains in a microbenchmark
+    (`measured_peaks`): key + "_of_measured". The dtype of a fraction comes
+    from the nearest enclosing key naming one (f32, bf16; fp64 otherwise)."""
+    ratio = {
+        "f64": PEAK["f64"] / (peaks["mfma_f64_TFLOPs"] * 1e12),
+        "f32": PEAK["f32"] / (peaks["mfma_f32_TFLOPs"] * 1e12),
+        "bf16": PEAK["bf16"] / (peaks["mfma_bf16_TFLOPs"] * 1e12),
+        "hbm": PEAK["hbm"] / (peaks["hbm_copy_GBps"] * 1e9),
+    }
+
+    def dtype_of(name, inherited):
+        for dt in ("bf16", "f32", "f64"):
+            if dt in name:
+                return dt
+        return inherited
+
+    def walk(d, dt):
+        for k, v in list(d.items()):
+            if isinstance(v, dict):
+                if k != "cpu":
+                    walk(v, dtype_of(k, dt))
+            elif isinstance(v, (int, float)) and not isinstance(v, bool):
+                if k in ("frac_mfma", "frac_binding_roofline", "ao_to_mo_frac_mfma"):
+                    d[k + "_of_measured"] = round(v * ratio[dt], 4)
+                elif k == "frac_mfma_f32":
+                    d[k + "_of_measured"] = round(v * ratio["f32"], 4)
+                elif k == "frac_hbm":
+                    d[k + "_of_measured"] = round(v * ratio["hbm"], 4)
+
+    walk(extra, "f64")
+
+
 def host_info(torch):
     model = "unknown"
     try:
@@ -322,6 +356,7 @@ def main():
             extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
         if "a5" in want:
             extra["a5_strided_patterns"] = bench_a5(torch, tt, dev, args)
+        add_measured_fractions(extra, peaks)
         line["configs"] = extra
 
     if not args.no_cpu:
@@ -606,11 +641,13 @@ def bench_c5(torch, tt, dev, args):
     V = (torch.randn(128, 128, 800, generator=g, dtype=torch.float64) * 0.1).to(dev)
     wall, ev_ms = timed_steady(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V), 3)
     flop = 2.62144e9 + 2 * 2.097152e12 + 2 * 2.62144e9
-    res = {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2), "path": "reference greedy [(0,1),(0,1),(0,1)]"}
+    res = {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
+           "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK["f64"], 4), "path": "reference greedy [(0,1),(0,1),(0,1)]"}
     # opt-in fewest-multiply-add order: 2*(1.6384e10 + 5.24288e9 + 51200) flop
     wall, ev_ms = timed_steady(torch, lambda: tt.einsum("ia,jb,abP,ijP->", A, B, W, V, optimize="optimal"), 10)
     flop = 2 * (1.6384e10 + 5.24288e9 + 51200)
     res["optimize_optimal"] = {"ms": round(ev_ms, 3), "TFLOP/s": round(flop / (ev_ms * 1e-3) / 1e12, 2),
+                               "frac_mfma": round(flop / (ev_ms * 1e-3) / PEAK["f64"], 4),
                                "path": "[(1,2),(1,2),(0,1)]", "speedup": round(res["ms"] / ev_ms, 1)}
     if not args.no_cpu:
         from oracle import cpu_ref
