@@ -501,6 +501,20 @@ def bench_c4_naux(torch, tt, dev, args):
             out[f"{key}_naux{naux}"] = {"ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                                         "frac_mfma": round(flop / (ms * 1e-3) / peak, 4)}
             del B, eo, ev
+    # A production-sized problem whose B (1.57 GB) does not fit the 256 MB
+    # MALL, so the panel re-reads that miss L2 go to HBM (inputs drawn on the
+    # device; same distributions as config 4).
+    print("bench: mp2 128x640x2400 fp64", file=sys.stderr, flush=True)
+    g = torch.Generator(device=dev).manual_seed(0)
+    B = torch.randn(128, 640, 2400, generator=g, device=dev, dtype=torch.float64) * 0.05
+    eo = torch.sort(-20 + 19.7 * torch.rand(128, generator=g, device=dev, dtype=torch.float64))[0]
+    ev = torch.sort(0.1 + 4.9 * torch.rand(640, generator=g, device=dev, dtype=torch.float64))[0]
+    _, ms = timed_steady(torch, lambda: tt.mp2_energy(B, eo, ev), 3)
+    flop = (128 * 129 // 2) * 2 * 640**2 * 2400
+    out["f64_nocc128_nvir640_naux2400"] = {"ms": round(ms, 2), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+                                           "frac_mfma": round(flop / (ms * 1e-3) / PEAK["f64"], 4),
+                                           "B_GB": round(B.numel() * 8 / 1e9, 2)}
+    del B, eo, ev
     # One GPU's share of an 8-GPU run at config 4 (fp64): each shard is a
     # contiguous eighth of the 31,200 work units (tt_mp2_energy_shard).
     print("bench: c4 shards of 8", file=sys.stderr, flush=True)
