@@ -1,8 +1,13 @@
-"""tt_mp2_energy_noalloc under HIP graph capture: the call allocates nothing
-and clears its accumulator with a kernel (no memset node), so it can be
-recorded once and replayed. Each replay, with eager work and new inputs in
-between, is checked against the eager tt_mp2_energy result on the same
-inputs (bitwise in deterministic mode)."""
+"""HIP graph capture: calls recorded once and replayed, each replay (with new
+inputs and eager work in between) checked against an eager call on the same
+inputs.
+
+- tt_mp2_energy_noalloc allocates nothing and clears its accumulator with a
+  kernel (no memset node); bitwise in deterministic mode.
+- einsum on GEMM, batched, strided, permutation, fused-path and 16-bit
+  contractions, and the public mp2_energy with and without its row-padded
+  copy of B: outputs and workspaces come from torch's graph pool; bitwise.
+"""
 
 import pytest
 import torch
@@ -112,3 +117,35 @@ def test_einsum_graph_replays(hip, sub, shapes, kw):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(res, want), (sub, k, (res.double() - want.double()).abs().max().item())
+
+
+@pytest.mark.parametrize("naux", [96, 37])
+def test_mp2_energy_graph_replays(hip, naux):
+    """The public mp2_energy recorded once under torch.cuda.graph: with naux
+    37 the call stages B into its workspace with rows padded to 48 elements
+    (a copy kernel, then the energy and the fixed-order sum), with naux 96 it
+    runs on B as given. Each replay, with new inputs and eager work in
+    between, equals an eager call bitwise."""
+    import trntensor_amd as tt
+
+    B, eo, ev = _inputs(0, naux=naux)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        tt.mp2_energy(B, eo, ev)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        res = tt.mp2_energy(B, eo, ev)
+    for k in range(3):
+        src = _inputs(k + 1, naux=naux)
+        B.copy_(src[0])
+        eo.copy_(src[1])
+        ev.copy_(src[2])
+        torch.cuda.synchronize()
+        want = float(tt.mp2_energy(B, eo, ev))
+        print(f"mp2_energy graph naux={naux} replay {k}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float(res) == want, (naux, k, float(res), want)
