@@ -177,6 +177,34 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
         }
     };
     auto compute = [&](int buf) {
+        if (NEED_Y && sizeof(T) == 8) {
+            // fp64: waves 0, 1 form X = P0 P1^T and waves 2, 3 Y = P2 P3^T,
+            // each a 64 x 32 half (columns ch .. ch + 31; row blocks 0, 1 in
+            // X[.][.], 2, 3 in Y[.][.]). A wave reads six fragments per stage
+            // for its 32 MFMAs instead of eight for quadrants of both (166 ->
+            // 158 VGPRs); the epilogue pairs X and Y through LDS. Config 4:
+            // 7.86-7.87 against 7.93 ms, energies bitwise equal. fp32 keeps the
+            // quadrants: the six fragments would cost it its fifth workgroup.
+            const int mat = wave >> 1;
+            const int ch = (wave & 1) * 32;
+            const T* rp = lds(buf, mat ? 2 : 0);
+            const T* cp = lds(buf, mat ? 3 : 1);
+            typename PN::vec_t fr[4], fc[2];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fr[a] = PN::frag(rp, 16 * a, lane);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) fc[b] = PN::frag(cp, ch + 16 * b, lane);
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        X[a][b] = MF::mma(fr[a][st], fc[b][st], X[a][b]);
+                        Y[a][b] = MF::mma(fr[a + 2][st], fc[b][st], Y[a][b]);
+                    }
+            return;
+        }
         typename PN::vec_t f0[2], f1[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a) f0[a] = PN::frag(lds(buf, 0), wr + 16 * a, lane);
@@ -326,6 +354,44 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
         mp2_kloop<T, BK, AW, false>(&lds[0][0][0], base0, base1, base2, base3, rows_p, rows_q, g.naux, X, Y);
 
     const int lg = lane >> 4;
+    // Rows and columns of the quadrant the energy loop below reads from X and Y.
+    int rb = wr, cb0 = wc;
+    if (sizeof(T) == 8 && ymode == 0) {
+        // The K loop left each fp64 X wave with X rows 0-63 of its columns
+        // and each Y wave with Y rows 0-63 of the same columns. The X wave
+        // keeps rows 0-31 and hands rows 32-63 to the Y wave, which keeps its
+        // rows 32-63 and hands rows 0-31 back, through LDS (free after the K
+        // loop's last barrier); each then holds X and Y of one quadrant.
+        const int mat = wave >> 1;
+        const int ch = (wave & 1) * 32;
+        constexpr int TP = kMp2Tile + 1;
+        T* xs = &lds[0][0][0];  // X rows 32-63
+        T* ys = xs + 32 * TP;   // Y rows 0-31
+        static_assert(kMp2Tile * TP <= 4 * PN::ELEMS, "exchange fits in the staging buffers");
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int o = (16 * a + MF::row(lg, r)) * TP + ch + 16 * b + (lane & 15);
+                    if (mat == 0) xs[o] = Y[a][b][r];
+                    else ys[o] = X[a][b][r];
+                }
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int o = (16 * a + MF::row(lg, r)) * TP + ch + 16 * b + (lane & 15);
+                    if (mat == 0) Y[a][b][r] = ys[o];
+                    else X[a][b][r] = xs[o];
+                }
+        rb = mat ? 32 : 0;
+        cb0 = ch;
+    }
     if (ymode == 2) {
         // Y = X^T through LDS (the staging buffers are free after the last barrier).
         constexpr int TP = kMp2Tile + 1;
@@ -359,27 +425,27 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     T e_bv[2], e_av[2][4];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        const int cb = wc + 16 * b + (lane & 15);
+        const int cb = cb0 + 16 * b + (lane & 15);
         e_bv[b] = ev[cb < rows_q ? q * kMp2Tile + cb : 0];
     }
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int ra = wr + 16 * a + MF::row(lg, r);
+            const int ra = rb + 16 * a + MF::row(lg, r);
             e_av[a][r] = ev[ra < rows_p ? p * kMp2Tile + ra : 0];
         }
     double sum = 0.0;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        const int cb = wc + 16 * b + (lane & 15);
+        const int cb = cb0 + 16 * b + (lane & 15);
         const bool okb = cb < rows_q;
         const T e_b = e_bv[b];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ra = wr + 16 * a + MF::row(lg, r);
+                const int ra = rb + 16 * a + MF::row(lg, r);
                 if (okb && ra < rows_p) {
                     const T e_a = e_av[a][r];
                     const T x = X[a][b][r];
