@@ -184,7 +184,9 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
             // for its 32 MFMAs instead of eight for quadrants of both (166 ->
             // 158 VGPRs); the epilogue pairs X and Y through LDS. Config 4:
             // 7.86-7.87 against 7.93 ms, energies bitwise equal. fp32 keeps the
-            // quadrants: the six fragments would cost it its fifth workgroup.
+            // quadrants: split, it needs 104 VGPRs (four workgroups per CU
+            // instead of five) and measured the same (4.145-4.150 against
+            // 4.146-4.158 ms).
             const int mat = wave >> 1;
             const int ch = (wave & 1) * 32;
             const T* rp = lds(buf, mat ? 2 : 0);
