@@ -1,7 +1,8 @@
 """The library launches on torch's current stream: work issued inside
 ``torch.cuda.stream(s)`` is queued on s (s reports pending work right after
 the call while the default stream is idle), ordered after s's earlier work,
-and its results equal the same call on the default stream."""
+and its results equal the same call on the default stream. Host threads on
+their own streams get the same results as single-threaded calls."""
 
 import pytest
 import torch
@@ -67,3 +68,50 @@ def test_side_stream_work_is_ordered_after_its_producer(hip):
     ref = tt.einsum("ij,jk->ik", ref_a, Y)
     torch.cuda.synchronize()
     assert torch.equal(C, ref)
+
+
+def test_threads_on_their_own_streams(hip):
+    """Four host threads, each on its own stream (torch's current stream is
+    per thread), run einsum and mp2_energy on their own inputs; every result
+    equals the same call made alone on the main thread."""
+    import threading
+
+    def inputs(seed):
+        g = torch.Generator().manual_seed(seed)
+        A = torch.randn(512, 384, generator=g, dtype=torch.float64).cuda()
+        Bm = torch.randn(384, 640, generator=g, dtype=torch.float64).cuda()
+        Bov = (torch.randn(6, 100, 97, generator=g, dtype=torch.float64) * 0.05).cuda()
+        eo = torch.sort(-20 + 19.7 * torch.rand(6, generator=g, dtype=torch.float64))[0].cuda()
+        ev = torch.sort(0.1 + 4.9 * torch.rand(100, generator=g, dtype=torch.float64))[0].cuda()
+        return A, Bm, Bov, eo, ev
+
+    def work(A, Bm, Bov, eo, ev):
+        return tt.einsum("ij,jk->ik", A, Bm), tt.mp2_energy(Bov, eo, ev)
+
+    data = [inputs(100 + t) for t in range(4)]
+    refs = [work(*d) for d in data]
+    torch.cuda.synchronize()
+    results = [[] for _ in data]
+    errors = []
+
+    def run(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(10):
+                    results[t].append(work(*data[t]))
+            s.synchronize()
+        except Exception as exc:  # reported on the main thread
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not errors, errors
+    for t, (gemm_ref, e_ref) in enumerate(refs):
+        assert len(results[t]) == 10
+        for gemm, e in results[t]:
+            assert torch.equal(gemm, gemm_ref)
+            assert torch.equal(e, e_ref)
