@@ -195,12 +195,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const int64_t nk = (g.K + BK - 1) / BK;
     // Stages 0 .. nfull-1 are interior for both operands.
     const int64_t nfull = (VEC && m0 + BM <= g.M && n0 + BN <= g.N) ? g.K / BK : 0;
-    auto load = [&](int64_t k0, auto fast) {
+    // The lambdas below are always inlined: left as calls (which the inliner
+    // chose for 64-deep stages), they capture acc by reference and the
+    // accumulators go to scratch memory.
+    auto load = [&](int64_t k0, auto fast) __attribute__((always_inline)) {
         constexpr bool F = decltype(fast)::value;
         sa.template load<F>(A, g.lda, m0, g.M, k0, g.K);
         sb.template load<F>(B, g.ldb, n0, g.N, k0, g.K);
     };
-    auto compute = [&](int buf) {
+    auto compute = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             T fa[FM][4], fb[FN][4];
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     // PRIO (fp64): the wave issuing a stage's MFMAs runs at raised priority
     // for the burst, so co-resident waves in their load/store phase do not
     // delay the MFMA stream.
-    auto mfma_stage = [&](int b) {
+    auto mfma_stage = [&](int b) __attribute__((always_inline)) {
         if (PRIO && sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
         compute(b);
         if (PRIO && sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
