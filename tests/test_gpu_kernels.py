@@ -104,6 +104,47 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
     assert _gemm_case(hip, dt, ta, tb, M, N, K, batch, 1.5, 0.5, True, seed=M + N, alias=True) <= TOL[dt]
 
 
+@pytest.mark.parametrize(
+    "N,K,batch,alpha,beta,with_c,ldd_pad",
+    [
+        (1024, 512, 1, 1.0, 0.0, False, 1),  # the AO->MO half transform's shape family
+        (2048, 64, 1, 1.5, 0.5, True, 1),
+        (512, 16, 3, 1.0, 0.25, True, 1),
+        (1024, 160, 2, -2.0, 1.0, True, 0),  # odd ldc/ldd: element stores
+    ],
+)
+def test_gemm_m64_direct_b_matches_lds_tile(hip, N, K, batch, alpha, beta, with_c, ldd_pad):
+    """fp64, M = 64, A transposed, B row-major, whole 128-column tiles: the
+    kernel that streams B straight into registers. Checked against float64
+    torch, and bitwise against the LDS-staged small-M tile, which computes the
+    same problem widened by one column (N + 1 is not a multiple of 128)."""
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(N + K + batch)
+    dev = torch.device("cuda")
+    M = 64
+    A = torch.randn(batch, K, M, generator=g, dtype=torch.float64)
+    B = torch.randn(batch, K, N + 1, generator=g, dtype=torch.float64)
+    ld = N + 1 + ldd_pad
+    C = torch.randn(batch, M, ld, generator=g, dtype=torch.float64)
+    ref = alpha * torch.bmm(A.transpose(1, 2), B[:, :, :N])
+    if with_c:
+        ref = ref + beta * C[:, :, :N]
+    Ad, Cd = A.to(dev), C.to(dev)
+    Bn = B[:, :, :N].contiguous().to(dev)  # ldb = N: the direct-B kernel
+    Bw = B.to(dev)  # ldb = N + 1, N + 1 columns: the LDS-staged tile
+    outs = []
+    for Bd, ldb, n in ((Bn, N, N), (Bw, N + 1, N + 1)):
+        D = torch.full((batch, M, ld), float("nan"), dtype=torch.float64, device=dev)
+        engine.gemm(True, False, M, n, K, Ad, M, K * M, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
+                    Cd if with_c else None, ld, M * ld)
+        outs.append(D)
+    torch.cuda.synchronize()
+    direct, staged = outs[0][:, :, :N], outs[1][:, :, :N]
+    assert normwise(direct.cpu(), ref) <= 1e-12
+    assert torch.equal(direct, staged)
+
+
 def test_gemm_k_zero_is_beta_c(hip):
     assert _gemm_case(hip, torch.float64, False, False, 9, 11, 0, 2, 1.5, 0.5, True) == 0.0
 

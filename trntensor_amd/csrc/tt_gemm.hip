@@ -385,6 +385,140 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// fp64 GEMM for M = 64 with op(A) = A^T stored [k][m] and B stored [k][n]
+// (the AO->MO half transform: M = nocc, K = nbasis, N = nbasis * naux), every
+// tile whole (N a multiple of 128, K of 16). A, re-read by every workgroup,
+// is staged through LDS (double-buffered, one barrier per 16-k stage); B,
+// streamed once, goes from memory (non-temporal) straight into the MFMA
+// operand registers, so only A's stages pass through LDS. Wave w owns all 64
+// rows and columns n0 + 32 w .. + 31; lane (g, c) feeds MFMA block b (0, 1)
+// with column n0 + 32 w + 2 c + b, so one 16-byte load per k-row gives it
+// both blocks' operand. MFMA step s of stage t gives lane group g the k index
+// 16 t + 4 g + s, the order of gemm_kernel, whose results it reproduces
+// bitwise. Four waves per SIMD (128 VGPRs; one value spills around the K loop)
+// against the LDS-staged tile: 64 x 786432 x 512 0.884-0.888 against
+// 0.917-0.921 ms on one box, alternating.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_m64_kernel(GemmArgs g) {
+    typedef double T;
+    typedef Mfma<T> MF;
+    typedef MF::acc_t acc_t;
+    typedef d2_t v2;
+    typedef Stage<T, 64, false, true, kBK> SA;  // A: 64 rows, row-contiguous, [k][m] in LDS
+    __shared__ __attribute__((aligned(16))) T lds[2 * SA::ELEMS];
+
+    const int64_t total = g.tiles_n * g.batch;
+    const int64_t id = xcd_remap(blockIdx.x, total);
+    const int64_t bat = id / g.tiles_n;
+    const int64_t tn = id - bat * g.tiles_n;
+    const T* A = static_cast<const T*>(g.A) + bat * g.sA;
+    const int64_t nk = g.K / kBK;
+
+    acc_t acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
+    {
+        const int lane = threadIdx.x & 63;
+        const int lg = lane >> 4;
+        const int c = lane & 15;
+        const T* B = static_cast<const T*>(g.B) + bat * g.sB + tn * 128 + (threadIdx.x >> 6) * 32 + 2 * c +
+                     (int64_t)(4 * lg) * g.ldb;
+        SA sa;
+        v2 rb[4];  // B operand of MFMA step s of the current stage
+        auto bload = [&](int64_t t, int s) __attribute__((always_inline)) {
+            rb[s] = __builtin_nontemporal_load(reinterpret_cast<const v2*>(B + (16 * t + s) * g.ldb));
+        };
+        auto step = [&](const T* sbuf, int s) __attribute__((always_inline)) {
+            T fa[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fa[a] = sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) acc[a][b] = MF::mma(fa[a], rb[s][b], acc[a][b]);
+        };
+        sa.template load<true>(A, g.lda, 0, 64, 0, g.K);
+        sa.store(lds);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bload(0, s);
+        __syncthreads();
+        int64_t t = 0;
+        for (; t + 1 < nk; ++t) {
+            // Stage t + 1 of A goes to the other buffer; step s's B operand is
+            // reloaded for stage t + 1 as soon as its MFMAs have issued. The
+            // wave issuing the MFMAs runs at raised priority for the burst.
+            sa.template load<true>(A, g.lda, 0, 64, (t + 1) * kBK, g.K);
+            const T* cur = lds + (t & 1) * SA::ELEMS;
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                step(cur, s);
+                bload(t + 1, s);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
+            __syncthreads();
+        }
+        const T* cur = lds + (t & 1) * SA::ELEMS;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) step(cur, s);
+    }
+
+    // D = alpha * acc (+ beta * C); acc[a][b][r] is row 16 a + lg + 4 r,
+    // column col + b. D and C rows start 16-byte aligned when their leading
+    // dimension is even (checked below), so a lane's two columns are one
+    // 16-byte piece. The lane indices are formed again here rather than held
+    // through the K loop.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lg = (tid & 63) >> 4;
+    const int64_t col = tn * 128 + (tid >> 6) * 32 + 2 * (tid & 15);
+    const T alpha = (T)g.alpha;
+    const T beta = (T)g.beta;
+    const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
+    T* D = static_cast<T*>(g.D) + bat * g.sD;
+    const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * 8)) & 15) == 0 &&
+                      (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * 8)) & 15) == 0);
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        T cv[4][2];
+        if (C) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) cv[r][b] = C[(16 * a + MF::row(lg, r)) * g.ldc + col + b];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            T v[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                v[b] = acc[a][b][r];
+                if (g.alpha != 1.0) v[b] = alpha * v[b];
+                if (C) v[b] = v[b] + beta * cv[r][b];
+            }
+            T* d = D + (16 * a + MF::row(lg, r)) * g.ldd + col;
+            if (vecd) {
+                *reinterpret_cast<v2*>(d) = v2{v[0], v[1]};
+            } else {
+                d[0] = v[0];
+                d[1] = v[1];
+            }
+        }
+    }
+}
+
+static int launch_m64(GemmArgs& g, hipStream_t st) {
+    g.tiles_m = 1;
+    g.tiles_n = g.N / 128;
+    const int64_t total = g.tiles_n * g.batch;
+    if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
+    hipLaunchKernelGGL(gemm_m64_kernel, dim3((unsigned)total), dim3(kThreads), 0, st, g);
+    return check_launch("tt_gemm");
+}
+
 template <typename T, int BM, int BN, int FM, int FN, bool DOT, int NBUF = 2, int BK = kBK, bool PRIO = false>
 static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) {
     g.tiles_m = (g.M + BM - 1) / BM;
@@ -429,6 +563,11 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // it stays on this tile only. This tile streams B (non-temporal loads), so
     // a B broadcast over the batch (stride 0, re-read per batch entry) takes
     // the two-buffer tile below.
+    // M = 64 exactly, A transposed and B row-major, whole tiles: A through
+    // LDS, B straight into registers (gemm_m64_kernel above).
+    if (sizeof(T) == 8 && !DOT && ta && !tb && vec && g.M == 64 && g.K > 0 && g.K % kBK == 0 && g.N % 128 == 0 &&
+        (g.batch == 1 || g.sB != 0))
+        return launch_m64(g, st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
