@@ -105,38 +105,44 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
 
 
 @pytest.mark.parametrize(
-    "N,K,batch,alpha,beta,with_c,ldd_pad",
+    "M,N,K,batch,alpha,beta,with_c,ldd_pad",
     [
-        (1024, 512, 1, 1.0, 0.0, False, 1),  # the AO->MO half transform's shape family
-        (2048, 64, 1, 1.5, 0.5, True, 1),
-        (512, 16, 3, 1.0, 0.25, True, 1),
-        (1024, 160, 2, -2.0, 1.0, True, 0),  # odd ldc/ldd: element stores
+        (64, 1024, 512, 1, 1.0, 0.0, False, 0),  # the AO->MO half transform's shape family
+        (64, 2048, 64, 1, 1.5, 0.5, True, 0),
+        (64, 512, 16, 3, 1.0, 0.25, True, 0),
+        (64, 1024, 160, 2, -2.0, 1.0, True, 1),  # odd ldc/ldd: element stores
+        (50, 1024, 500, 1, 1.0, 0.0, False, 0),  # M < 64, K tail
+        (33, 1152, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
+        (1, 256, 31, 1, 1.0, 0.0, False, 0),
+        (64, 1030, 48, 1, 1.0, 0.5, True, 0),  # N not a multiple of 128: the LDS-staged tile in both runs
     ],
 )
-def test_gemm_m64_direct_b_matches_lds_tile(hip, N, K, batch, alpha, beta, with_c, ldd_pad):
-    """fp64, M = 64, A transposed, B row-major, whole 128-column tiles: the
+def test_gemm_m64_direct_b_matches_lds_tile(hip, M, N, K, batch, alpha, beta, with_c, ldd_pad):
+    """fp64, M <= 64, A transposed, B row-major, N a multiple of 128: the
     kernel that streams B straight into registers. Checked against float64
-    torch, and bitwise against the LDS-staged small-M tile, which computes the
-    same problem widened by one column (N + 1 is not a multiple of 128)."""
+    torch, and bitwise against the LDS-staged tile, which the same problem
+    takes when B's leading dimension is odd (no 16-byte vector path)."""
     from trntensor_amd.hip import engine
 
-    g = torch.Generator().manual_seed(N + K + batch)
+    g = torch.Generator().manual_seed(M + N + K + batch)
     dev = torch.device("cuda")
-    M = 64
-    A = torch.randn(batch, K, M, generator=g, dtype=torch.float64)
-    B = torch.randn(batch, K, N + 1, generator=g, dtype=torch.float64)
-    ld = N + 1 + ldd_pad
+    ldb_odd = N + 1 if (N + 1) % 2 else N + 2
+    lda = M + M % 2  # even: A's 16-byte vector path
+    A = torch.randn(batch, K, lda, generator=g, dtype=torch.float64)
+    B = torch.randn(batch, K, ldb_odd, generator=g, dtype=torch.float64)
+    ld = N + 1 + N % 2 if ldd_pad else N + 2 - N % 2  # odd (element stores) or even, above N
+    ldb_even = N + N % 2
     C = torch.randn(batch, M, ld, generator=g, dtype=torch.float64)
-    ref = alpha * torch.bmm(A.transpose(1, 2), B[:, :, :N])
+    ref = alpha * torch.bmm(A[:, :, :M].transpose(1, 2), B[:, :, :N])
     if with_c:
         ref = ref + beta * C[:, :, :N]
     Ad, Cd = A.to(dev), C.to(dev)
-    Bn = B[:, :, :N].contiguous().to(dev)  # ldb = N: the direct-B kernel
-    Bw = B.to(dev)  # ldb = N + 1, N + 1 columns: the LDS-staged tile
+    Bn = B[:, :, :ldb_even].contiguous().to(dev)  # even ldb: the direct-B kernel on whole tiles
+    Bo = B.to(dev)  # odd ldb: the LDS-staged tile only
     outs = []
-    for Bd, ldb, n in ((Bn, N, N), (Bw, N + 1, N + 1)):
+    for Bd, ldb in ((Bn, ldb_even), (Bo, ldb_odd)):
         D = torch.full((batch, M, ld), float("nan"), dtype=torch.float64, device=dev)
-        engine.gemm(True, False, M, n, K, Ad, M, K * M, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
+        engine.gemm(True, False, M, N, K, Ad, lda, K * lda, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
                     Cd if with_c else None, ld, M * ld)
         outs.append(D)
     torch.cuda.synchronize()

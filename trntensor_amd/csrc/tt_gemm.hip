@@ -385,19 +385,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// fp64 GEMM for M = 64 with op(A) = A^T stored [k][m] and B stored [k][n]
-// (the AO->MO half transform: M = nocc, K = nbasis, N = nbasis * naux), every
-// tile whole (N a multiple of 128, K of 16). A, re-read by every workgroup,
-// is staged through LDS (double-buffered, one barrier per 16-k stage); B,
-// streamed once, goes from memory (non-temporal) straight into the MFMA
-// operand registers, so only A's stages pass through LDS. Wave w owns all 64
-// rows and columns n0 + 32 w .. + 31; lane (g, c) feeds MFMA block b (0, 1)
-// with column n0 + 32 w + 2 c + b, so one 16-byte load per k-row gives it
-// both blocks' operand. MFMA step s of stage t gives lane group g the k index
-// 16 t + 4 g + s, the order of gemm_kernel, whose results it reproduces
-// bitwise. Four waves per SIMD (128 VGPRs; one value spills around the K loop)
-// against the LDS-staged tile: 64 x 786432 x 512 0.884-0.888 against
-// 0.917-0.921 ms on one box, alternating.
+// fp64 GEMM for M <= 64 with op(A) = A^T stored [k][m] and B stored [k][n]
+// (the AO->MO half transform: M = nocc, K = nbasis, N = nbasis * naux), N a
+// multiple of 128 (whole tiles). A, re-read by every workgroup, is staged through LDS
+// (double-buffered, one barrier per 16-k stage; rows from M up and k from K
+// up read as zero); B, streamed once, goes from memory (non-temporal) straight
+// into the MFMA operand registers, so only A's stages pass through LDS. Wave w
+// owns all 64 rows and columns n0 + 32 w .. + 31; lane (g, c) feeds MFMA block
+// b (0, 1) with column n0 + 32 w + 2 c + b, so one 16-byte load per k-row
+// gives it both blocks' operand. MFMA step s of stage t gives lane group g
+// the k index 16 t + 4 g + s, the order of gemm_kernel, whose results it
+// reproduces bitwise. Four waves per SIMD (124-128 VGPRs) against the
+// LDS-staged tile's four: 64 x 786432 x 512 0.877-0.883 against 0.893-0.900 ms
+// on one box and 0.885-0.886 against 0.913-0.915 ms on another, alternating;
+// M < 64 (48 x 65536 x 256, four batches) measured the same on both.
+template <bool FULLM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_m64_kernel(GemmArgs g) {
     typedef double T;
     typedef Mfma<T> MF;
@@ -411,14 +413,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int64_t bat = id / g.tiles_n;
     const int64_t tn = id - bat * g.tiles_n;
     const T* A = static_cast<const T*>(g.A) + bat * g.sA;
-    const int64_t nk = g.K / kBK;
+    const int64_t nk = (g.K + kBK - 1) / kBK;
+    const int64_t nfull = g.K / kBK;
 
     acc_t acc[4][2];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
-    {
+    if (nk > 0) {
         const int lane = threadIdx.x & 63;
         const int lg = lane >> 4;
         const int c = lane & 15;
@@ -429,6 +432,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         auto bload = [&](int64_t t, int s) __attribute__((always_inline)) {
             rb[s] = __builtin_nontemporal_load(reinterpret_cast<const v2*>(B + (16 * t + s) * g.ldb));
         };
+        // Stage t's B where it may pass K: k-rows from K up read as zero.
+        auto bload_tail = [&](int64_t t, int s) __attribute__((always_inline)) {
+            const bool ok = 16 * t + 4 * lg + s < g.K;
+            const v2 x = *reinterpret_cast<const v2*>(ok ? B + (16 * t + s) * g.ldb : B - (int64_t)(4 * lg) * g.ldb);
+            rb[s] = ok ? x : v2{0.0, 0.0};
+        };
+        auto aload = [&](int64_t t) __attribute__((always_inline)) {
+            if (FULLM && t < nfull) sa.template load<true>(A, g.lda, 0, 64, t * kBK, g.K);
+            else sa.template load<false>(A, g.lda, 0, g.M, t * kBK, g.K);
+        };
         auto step = [&](const T* sbuf, int s) __attribute__((always_inline)) {
             T fa[4];
 #pragma unroll
@@ -438,17 +451,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                 for (int b = 0; b < 2; ++b) acc[a][b] = MF::mma(fa[a], rb[s][b], acc[a][b]);
         };
-        sa.template load<true>(A, g.lda, 0, 64, 0, g.K);
+        aload(0);
         sa.store(lds);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bload(0, s);
+        for (int s = 0; s < 4; ++s) {
+            if (nfull > 0) bload(0, s);
+            else bload_tail(0, s);
+        }
         __syncthreads();
         int64_t t = 0;
-        for (; t + 1 < nk; ++t) {
+        for (; t + 1 < nfull; ++t) {
             // Stage t + 1 of A goes to the other buffer; step s's B operand is
             // reloaded for stage t + 1 as soon as its MFMAs have issued. The
             // wave issuing the MFMAs runs at raised priority for the burst.
-            sa.template load<true>(A, g.lda, 0, 64, (t + 1) * kBK, g.K);
+            aload(t + 1);
             const T* cur = lds + (t & 1) * SA::ELEMS;
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -460,6 +476,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             __builtin_amdgcn_sched_barrier(0);
             sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
             __syncthreads();
+        }
+        if (t + 1 < nk) {
+            // The partial last stage (K not a multiple of 16).
+            aload(t + 1);
+            const T* cur = lds + (t & 1) * SA::ELEMS;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                step(cur, s);
+                bload_tail(t + 1, s);
+            }
+            sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
+            __syncthreads();
+            ++t;
         }
         const T* cur = lds + (t & 1) * SA::ELEMS;
 #pragma unroll
@@ -486,12 +515,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         T cv[4][2];
         if (C) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = 16 * a + MF::row(lg, r);
+                const bool ok = FULLM || row < g.M;
 #pragma unroll
-                for (int b = 0; b < 2; ++b) cv[r][b] = C[(16 * a + MF::row(lg, r)) * g.ldc + col + b];
+                for (int b = 0; b < 2; ++b) {
+                    const T x = C[ok ? row * g.ldc + col + b : 0];
+                    cv[r][b] = ok ? x : T(0);
+                }
+            }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            const int64_t row = 16 * a + MF::row(lg, r);
+            if (!FULLM && row >= g.M) continue;
             T v[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
@@ -499,7 +536,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 if (g.alpha != 1.0) v[b] = alpha * v[b];
                 if (C) v[b] = v[b] + beta * cv[r][b];
             }
-            T* d = D + (16 * a + MF::row(lg, r)) * g.ldd + col;
+            T* d = D + row * g.ldd + col;
             if (vecd) {
                 *reinterpret_cast<v2*>(d) = v2{v[0], v[1]};
             } else {
@@ -515,7 +552,8 @@ static int launch_m64(GemmArgs& g, hipStream_t st) {
     g.tiles_n = g.N / 128;
     const int64_t total = g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
-    hipLaunchKernelGGL(gemm_m64_kernel, dim3((unsigned)total), dim3(kThreads), 0, st, g);
+    if (g.M == 64) hipLaunchKernelGGL(gemm_m64_kernel<true>, dim3((unsigned)total), dim3(kThreads), 0, st, g);
+    else hipLaunchKernelGGL(gemm_m64_kernel<false>, dim3((unsigned)total), dim3(kThreads), 0, st, g);
     return check_launch("tt_gemm");
 }
 
@@ -563,11 +601,13 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // it stays on this tile only. This tile streams B (non-temporal loads), so
     // a B broadcast over the batch (stride 0, re-read per batch entry) takes
     // the two-buffer tile below.
-    // M = 64 exactly, A transposed and B row-major, whole tiles: A through
-    // LDS, B straight into registers (gemm_m64_kernel above).
-    if (sizeof(T) == 8 && !DOT && ta && !tb && vec && g.M == 64 && g.K > 0 && g.K % kBK == 0 && g.N % 128 == 0 &&
-        (g.batch == 1 || g.sB != 0))
-        return launch_m64(g, st);
+    // M <= 64, A transposed and B row-major, N a multiple of 128: A through
+    // LDS, B straight into registers (gemm_m64_kernel above). With N % 128
+    // columns left over, a second launch for them ran alone after the first
+    // (nocc 50, N = 100002: 0.198 against 0.146 ms), so such shapes stay on
+    // the LDS-staged tile below.
+    if constexpr (sizeof(T) == 8 && !DOT)
+        if (ta && !tb && vec && g.M <= 64 && g.N % 128 == 0 && (g.batch == 1 || g.sB != 0)) return launch_m64(g, st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
