@@ -105,44 +105,53 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
 
 
 @pytest.mark.parametrize(
-    "M,N,K,batch,alpha,beta,with_c,ldd_pad",
+    "ta,M,N,K,batch,alpha,beta,with_c,ldd_pad",
     [
-        (64, 1024, 512, 1, 1.0, 0.0, False, 0),  # the AO->MO half transform's shape family
-        (64, 2048, 64, 1, 1.5, 0.5, True, 0),
-        (64, 512, 16, 3, 1.0, 0.25, True, 0),
-        (64, 1024, 160, 2, -2.0, 1.0, True, 1),  # odd ldc/ldd: element stores
-        (50, 1024, 500, 1, 1.0, 0.0, False, 0),  # M < 64, K tail
-        (33, 1152, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
-        (1, 256, 31, 1, 1.0, 0.0, False, 0),
-        (64, 1030, 48, 1, 1.0, 0.5, True, 0),  # N not a multiple of 128: the LDS-staged tile in both runs
+        (True, 64, 1024, 512, 1, 1.0, 0.0, False, 0),  # the AO->MO half transform's shape family
+        (True, 64, 2048, 64, 1, 1.5, 0.5, True, 0),
+        (True, 64, 512, 16, 3, 1.0, 0.25, True, 0),
+        (True, 64, 1024, 160, 2, -2.0, 1.0, True, 1),  # odd ldc/ldd: element stores
+        (True, 50, 1024, 500, 1, 1.0, 0.0, False, 0),  # M < 64, K tail
+        (True, 33, 1152, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
+        (True, 1, 256, 31, 1, 1.0, 0.0, False, 0),
+        (True, 64, 1030, 48, 1, 1.0, 0.5, True, 0),  # N not a multiple of 128: the LDS-staged tile in both runs
+        # batched, B cached (64-row slabs of A, either layout)
+        (False, 512, 512, 512, 4, 1.5, 0.5, True, 0),  # the 64 x 512^3 batch's shape
+        (True, 512, 512, 512, 3, 1.0, 0.0, False, 0),
+        (True, 320, 1536, 512, 2, 1.0, 0.0, False, 0),  # the AO->MO transform's second GEMM
+        (False, 200, 256, 333, 3, -1.0, 1.0, True, 1),  # ragged M and K
+        (True, 70, 384, 1000, 2, 2.0, 0.0, False, 0),
     ],
 )
-def test_gemm_m64_direct_b_matches_lds_tile(hip, M, N, K, batch, alpha, beta, with_c, ldd_pad):
-    """fp64, M <= 64, A transposed, B row-major, N a multiple of 128: the
-    kernel that streams B straight into registers. Checked against float64
-    torch, and bitwise against the LDS-staged tile, which the same problem
-    takes when B's leading dimension is odd (no 16-byte vector path)."""
+def test_gemm_direct_b_matches_lds_tile(hip, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
+    """fp64, B row-major, N a multiple of 128: the kernel that loads B straight
+    into the MFMA registers (M <= 64 with A transposed, or batched with K <=
+    1024). Checked against float64 torch, and bitwise against the LDS-staged
+    tiles, which the same problem takes when B's leading dimension is odd (no
+    16-byte vector path)."""
     from trntensor_amd.hip import engine
 
-    g = torch.Generator().manual_seed(M + N + K + batch)
+    g = torch.Generator().manual_seed(M + N + K + batch + int(ta))
     dev = torch.device("cuda")
     ldb_odd = N + 1 if (N + 1) % 2 else N + 2
-    lda = M + M % 2  # even: A's 16-byte vector path
-    A = torch.randn(batch, K, lda, generator=g, dtype=torch.float64)
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    lda = a_cols + a_cols % 2  # even: A's 16-byte vector path
+    A = torch.randn(batch, a_rows, lda, generator=g, dtype=torch.float64)
     B = torch.randn(batch, K, ldb_odd, generator=g, dtype=torch.float64)
     ld = N + 1 + N % 2 if ldd_pad else N + 2 - N % 2  # odd (element stores) or even, above N
     ldb_even = N + N % 2
     C = torch.randn(batch, M, ld, generator=g, dtype=torch.float64)
-    ref = alpha * torch.bmm(A[:, :, :M].transpose(1, 2), B[:, :, :N])
+    opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
+    ref = alpha * torch.bmm(opA, B[:, :, :N])
     if with_c:
         ref = ref + beta * C[:, :, :N]
     Ad, Cd = A.to(dev), C.to(dev)
-    Bn = B[:, :, :ldb_even].contiguous().to(dev)  # even ldb: the direct-B kernel on whole tiles
-    Bo = B.to(dev)  # odd ldb: the LDS-staged tile only
+    Bn = B[:, :, :ldb_even].contiguous().to(dev)  # even ldb: the direct-B kernel
+    Bo = B.to(dev)  # odd ldb: the LDS-staged tiles only
     outs = []
     for Bd, ldb in ((Bn, ldb_even), (Bo, ldb_odd)):
         D = torch.full((batch, M, ld), float("nan"), dtype=torch.float64, device=dev)
-        engine.gemm(True, False, M, N, K, Ad, lda, K * lda, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
+        engine.gemm(ta, False, M, N, K, Ad, lda, a_rows * lda, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
                     Cd if with_c else None, ld, M * ld)
         outs.append(D)
     torch.cuda.synchronize()

@@ -385,33 +385,38 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// fp64 GEMM for M <= 64 with op(A) = A^T stored [k][m] and B stored [k][n]
-// (the AO->MO half transform: M = nocc, K = nbasis, N = nbasis * naux), N a
-// multiple of 128 (whole tiles). A, re-read by every workgroup, is staged through LDS
-// (double-buffered, one barrier per 16-k stage; rows from M up and k from K
-// up read as zero); B, streamed once, goes from memory (non-temporal) straight
-// into the MFMA operand registers, so only A's stages pass through LDS. Wave w
-// owns all 64 rows and columns n0 + 32 w .. + 31; lane (g, c) feeds MFMA block
-// b (0, 1) with column n0 + 32 w + 2 c + b, so one 16-byte load per k-row
-// gives it both blocks' operand. MFMA step s of stage t gives lane group g
-// the k index 16 t + 4 g + s, the order of gemm_kernel, whose results it
-// reproduces bitwise. Four waves per SIMD (124-128 VGPRs) against the
-// LDS-staged tile's four: 64 x 786432 x 512 0.877-0.883 against 0.893-0.900 ms
-// on one box and 0.885-0.886 against 0.913-0.915 ms on another, alternating;
-// M < 64 (48 x 65536 x 256, four batches) measured the same on both.
-template <bool FULLM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_m64_kernel(GemmArgs g) {
+// fp64 GEMM with B stored [k][n] (row-major) and N a multiple of 128, on
+// 64 x 128 tiles of four waves. A (either layout) is staged through LDS one
+// 64-row slab per workgroup, double-buffered, one barrier per 16-k stage;
+// rows from M up and k from K up read as zero. B goes from memory straight
+// into the MFMA operand registers: wave w owns all 64 rows and columns
+// n0 + 32 w .. + 31, and lane (g, c) feeds MFMA block b (0, 1) with column
+// n0 + 32 w + 2 c + b, so one 16-byte load per k-row gives it both blocks'
+// operand, and B never passes through LDS. MFMA step s of stage t gives lane
+// group g the k index 16 t + 4 g + s, the order of gemm_kernel, whose results
+// it reproduces bitwise. 123-128 VGPRs: four waves per SIMD. NT: B is read
+// once (M <= 64, the AO->MO half transform), so its loads bypass the caches.
+// AO->MO half transform (64 x 786432 x 512) against the LDS-staged small-M
+// tile: 0.877-0.883 against 0.893-0.900 ms on one box and 0.885-0.886 against
+// 0.913-0.915 ms on another, alternating; M < 64 (48 x 65536 x 256, four
+// batches) measured the same.
+template <bool FULLM, bool TA, bool NT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_directb_kernel(GemmArgs g) {
     typedef double T;
     typedef Mfma<T> MF;
     typedef MF::acc_t acc_t;
     typedef d2_t v2;
-    typedef Stage<T, 64, false, true, kBK> SA;  // A: 64 rows, row-contiguous, [k][m] in LDS
+    typedef Stage<T, 64, !TA, true, kBK> SA;  // A: a 64-row slab, [k][m] (TA) or [m][k] in LDS
     __shared__ __attribute__((aligned(16))) T lds[2 * SA::ELEMS];
 
-    const int64_t total = g.tiles_n * g.batch;
-    const int64_t id = xcd_remap(blockIdx.x, total);
-    const int64_t bat = id / g.tiles_n;
-    const int64_t tn = id - bat * g.tiles_n;
+    // Tile order: the 64-row slabs of one column tile are adjacent (they
+    // share its B panel in L2).
+    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t id = xcd_remap(blockIdx.x, tiles * g.batch);
+    const int64_t bat = id / tiles;
+    const int64_t rem = id - bat * tiles;
+    const int64_t tn = rem / g.tiles_m;
+    const int64_t m0 = (rem - tn * g.tiles_m) * 64;
     const T* A = static_cast<const T*>(g.A) + bat * g.sA;
     const int64_t nk = (g.K + kBK - 1) / kBK;
     const int64_t nfull = g.K / kBK;
@@ -430,7 +435,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         SA sa;
         v2 rb[4];  // B operand of MFMA step s of the current stage
         auto bload = [&](int64_t t, int s) __attribute__((always_inline)) {
-            rb[s] = __builtin_nontemporal_load(reinterpret_cast<const v2*>(B + (16 * t + s) * g.ldb));
+            const v2* q = reinterpret_cast<const v2*>(B + (16 * t + s) * g.ldb);
+            rb[s] = NT ? __builtin_nontemporal_load(q) : *q;
         };
         // Stage t's B where it may pass K: k-rows from K up read as zero.
         auto bload_tail = [&](int64_t t, int s) __attribute__((always_inline)) {
@@ -439,13 +445,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             rb[s] = ok ? x : v2{0.0, 0.0};
         };
         auto aload = [&](int64_t t) __attribute__((always_inline)) {
-            if (FULLM && t < nfull) sa.template load<true>(A, g.lda, 0, 64, t * kBK, g.K);
-            else sa.template load<false>(A, g.lda, 0, g.M, t * kBK, g.K);
+            if (FULLM && t < nfull) sa.template load<true>(A, g.lda, m0, g.M, t * kBK, g.K);
+            else sa.template load<false>(A, g.lda, m0, g.M, t * kBK, g.K);
         };
         auto step = [&](const T* sbuf, int s) __attribute__((always_inline)) {
             T fa[4];
 #pragma unroll
-            for (int a = 0; a < 4; ++a) fa[a] = sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c];
+            for (int a = 0; a < 4; ++a)
+                fa[a] = TA ? sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c] : sbuf[(16 * a + c) * SA::PITCH + 4 * lg + s];
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -516,7 +523,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (C) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = 16 * a + MF::row(lg, r);
+                const int64_t row = m0 + 16 * a + MF::row(lg, r);
                 const bool ok = FULLM || row < g.M;
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
@@ -527,7 +534,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t row = 16 * a + MF::row(lg, r);
+            const int64_t row = m0 + 16 * a + MF::row(lg, r);
             if (!FULLM && row >= g.M) continue;
             T v[2];
 #pragma unroll
@@ -547,13 +554,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
 }
 
-static int launch_m64(GemmArgs& g, hipStream_t st) {
-    g.tiles_m = 1;
+static int launch_directb(GemmArgs& g, bool ta, bool nt, hipStream_t st) {
+    g.tiles_m = (g.M + 63) / 64;
     g.tiles_n = g.N / 128;
-    const int64_t total = g.tiles_n * g.batch;
+    const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
-    if (g.M == 64) hipLaunchKernelGGL(gemm_m64_kernel<true>, dim3((unsigned)total), dim3(kThreads), 0, st, g);
-    else hipLaunchKernelGGL(gemm_m64_kernel<false>, dim3((unsigned)total), dim3(kThreads), 0, st, g);
+    const bool full = g.M % 64 == 0;
+    const dim3 grid((unsigned)total), block(kThreads);
+#define TT_DIRECTB_CASE(F, A_T, N_T) \
+    if (full == F && ta == A_T && nt == N_T) hipLaunchKernelGGL((gemm_directb_kernel<F, A_T, N_T>), grid, block, 0, st, g);
+    TT_DIRECTB_CASE(true, true, true)
+    TT_DIRECTB_CASE(false, true, true)
+    TT_DIRECTB_CASE(true, true, false)
+    TT_DIRECTB_CASE(false, true, false)
+    TT_DIRECTB_CASE(true, false, false)
+    TT_DIRECTB_CASE(false, false, false)
+#undef TT_DIRECTB_CASE
     return check_launch("tt_gemm");
 }
 
@@ -602,12 +618,21 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // a B broadcast over the batch (stride 0, re-read per batch entry) takes
     // the two-buffer tile below.
     // M <= 64, A transposed and B row-major, N a multiple of 128: A through
-    // LDS, B straight into registers (gemm_m64_kernel above). With N % 128
+    // LDS, B straight into registers (gemm_directb_kernel above). With N % 128
     // columns left over, a second launch for them ran alone after the first
     // (nocc 50, N = 100002: 0.198 against 0.146 ms), so such shapes stay on
     // the LDS-staged tile below.
     if constexpr (sizeof(T) == 8 && !DOT)
-        if (ta && !tb && vec && g.M <= 64 && g.N % 128 == 0 && (g.batch == 1 || g.sB != 0)) return launch_m64(g, st);
+        if (ta && !tb && vec && g.M <= 64 && g.N % 128 == 0 && (g.batch == 1 || g.sB != 0))
+            return launch_directb(g, true, true, st);
+    // Batched short-K fp64 with B row-major (e.g. 64 x 512^3, the AO->MO
+    // transform's second GEMM): the same kernel on 64-row slabs, B cached (each
+    // B panel serves M / 64 slabs). Same box, alternating, bitwise equal, against
+    // the LDS-staged 64 x 128 tile: 64 x 512^3 with alpha/beta and C 0.275
+    // against 0.290 ms (NN) and 0.267 against 0.287 ms (TN); 64 x (320 x 1536 x
+    // 512) TN 0.485 against 0.510 ms.
+    if constexpr (sizeof(T) == 8 && !DOT)
+        if (!tb && vec && g.batch > 1 && g.K <= 1024 && g.N % 128 == 0) return launch_directb(g, ta, false, st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
