@@ -567,6 +567,8 @@ static int launch_directb(GemmArgs& g, bool ta, bool nt, hipStream_t st) {
     TT_DIRECTB_CASE(false, true, true)
     TT_DIRECTB_CASE(true, true, false)
     TT_DIRECTB_CASE(false, true, false)
+    TT_DIRECTB_CASE(true, false, true)
+    TT_DIRECTB_CASE(false, false, true)
     TT_DIRECTB_CASE(true, false, false)
     TT_DIRECTB_CASE(false, false, false)
 #undef TT_DIRECTB_CASE
@@ -617,22 +619,19 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // it stays on this tile only. This tile streams B (non-temporal loads), so
     // a B broadcast over the batch (stride 0, re-read per batch entry) takes
     // the two-buffer tile below.
-    // M <= 64, A transposed and B row-major, N a multiple of 128: A through
-    // LDS, B straight into registers (gemm_directb_kernel above). With N % 128
-    // columns left over, a second launch for them ran alone after the first
-    // (nocc 50, N = 100002: 0.198 against 0.146 ms), so such shapes stay on
-    // the LDS-staged tile below.
+    // fp64 with B row-major and N a multiple of 128: A through LDS, B straight
+    // into the MFMA registers (gemm_directb_kernel above), non-temporal when
+    // B is read once (M <= 64). Same box, alternating, bitwise equal, against
+    // the LDS-staged tiles below: 4096^3 with alpha/beta 1.952 against 2.082
+    // ms (NN 1.944 against 2.069, TN 1.965 against 2.171), 4096^2 x 512 0.258
+    // against 0.274 ms, 64 x 512^3 with alpha/beta and C 0.275 against 0.292
+    // ms, the AO->MO transform's two GEMMs 0.885 against 0.914 and 0.492
+    // against 0.520 ms. With N % 128 columns left over, a second launch for
+    // them ran alone after the first (nocc 50, N = 100002: 0.198 against
+    // 0.146 ms), so such shapes stay on the LDS-staged tiles.
     if constexpr (sizeof(T) == 8 && !DOT)
-        if (ta && !tb && vec && g.M <= 64 && g.N % 128 == 0 && (g.batch == 1 || g.sB != 0))
-            return launch_directb(g, true, true, st);
-    // Batched short-K fp64 with B row-major (e.g. 64 x 512^3, the AO->MO
-    // transform's second GEMM): the same kernel on 64-row slabs, B cached (each
-    // B panel serves M / 64 slabs). Same box, alternating, bitwise equal, against
-    // the LDS-staged 64 x 128 tile: 64 x 512^3 with alpha/beta and C 0.275
-    // against 0.290 ms (NN) and 0.267 against 0.287 ms (TN); 64 x (320 x 1536 x
-    // 512) TN 0.485 against 0.510 ms.
-    if constexpr (sizeof(T) == 8 && !DOT)
-        if (!tb && vec && g.batch > 1 && g.K <= 1024 && g.N % 128 == 0) return launch_directb(g, ta, false, st);
+        if (!tb && vec && g.N % 128 == 0)
+            return launch_directb(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
