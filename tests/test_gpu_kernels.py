@@ -104,6 +104,7 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
     assert _gemm_case(hip, dt, ta, tb, M, N, K, batch, 1.5, 0.5, True, seed=M + N, alias=True) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
 @pytest.mark.parametrize(
     "ta,M,N,K,batch,alpha,beta,with_c,ldd_pad",
     [
@@ -123,40 +124,41 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
         (True, 70, 384, 1000, 2, 2.0, 0.0, False, 0),
     ],
 )
-def test_gemm_direct_b_matches_lds_tile(hip, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
-    """fp64, B row-major, N a multiple of 128: the kernel that loads B straight
-    into the MFMA registers (M <= 64 with A transposed, or batched with K <=
-    1024). Checked against float64 torch, and bitwise against the LDS-staged
-    tiles, which the same problem takes when B's leading dimension is odd (no
-    16-byte vector path)."""
+def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
+    """B row-major, N a multiple of 128 (fp64) or 256 (fp32): the kernel that
+    loads B straight into the MFMA registers. Checked against float64 torch,
+    and bitwise against the LDS-staged tiles, which the same problem takes when
+    B's leading dimension breaks 16-byte alignment (no vector path)."""
     from trntensor_amd.hip import engine
 
     g = torch.Generator().manual_seed(M + N + K + batch + int(ta))
     dev = torch.device("cuda")
+    V = 16 // torch.tensor([], dtype=dt).element_size()  # elements per 16 bytes
+    up = lambda n: n + (-n) % V  # noqa: E731
     ldb_odd = N + 1 if (N + 1) % 2 else N + 2
     a_rows, a_cols = (K, M) if ta else (M, K)
-    lda = a_cols + a_cols % 2  # even: A's 16-byte vector path
+    lda = up(a_cols)  # A's 16-byte vector path
+    ldb_even = up(N)
     A = torch.randn(batch, a_rows, lda, generator=g, dtype=torch.float64)
-    B = torch.randn(batch, K, ldb_odd, generator=g, dtype=torch.float64)
-    ld = N + 1 + N % 2 if ldd_pad else N + 2 - N % 2  # odd (element stores) or even, above N
-    ldb_even = N + N % 2
+    B = torch.randn(batch, K, max(ldb_odd, ldb_even), generator=g, dtype=torch.float64)
+    ld = up(N + 1) + 1 if ldd_pad else up(N + 1)  # unaligned (element stores) or aligned, above N
     C = torch.randn(batch, M, ld, generator=g, dtype=torch.float64)
     opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
     ref = alpha * torch.bmm(opA, B[:, :, :N])
     if with_c:
         ref = ref + beta * C[:, :, :N]
-    Ad, Cd = A.to(dev), C.to(dev)
-    Bn = B[:, :, :ldb_even].contiguous().to(dev)  # even ldb: the direct-B kernel
-    Bo = B.to(dev)  # odd ldb: the LDS-staged tiles only
+    Ad, Cd = A.to(dev, dt), C.to(dev, dt)
+    Bn = B[:, :, :ldb_even].contiguous().to(dev, dt)  # aligned ldb: the direct-B kernel
+    Bo = B[:, :, :ldb_odd].contiguous().to(dev, dt)  # odd ldb: the LDS-staged tiles only
     outs = []
     for Bd, ldb in ((Bn, ldb_even), (Bo, ldb_odd)):
-        D = torch.full((batch, M, ld), float("nan"), dtype=torch.float64, device=dev)
+        D = torch.full((batch, M, ld), float("nan"), dtype=dt, device=dev)
         engine.gemm(ta, False, M, N, K, Ad, lda, a_rows * lda, Bd, ldb, K * ldb, D, ld, M * ld, batch, alpha, beta,
                     Cd if with_c else None, ld, M * ld)
         outs.append(D)
     torch.cuda.synchronize()
     direct, staged = outs[0][:, :, :N], outs[1][:, :, :N]
-    assert normwise(direct.cpu(), ref) <= 1e-12
+    assert normwise(direct.cpu().double(), ref) <= TOL[dt]
     assert torch.equal(direct, staged)
 
 

@@ -385,27 +385,29 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// fp64 GEMM with B stored [k][n] (row-major) and N a multiple of 128, on
-// 64 x 128 tiles of four waves. A (either layout) is staged through LDS one
-// 64-row slab per workgroup, double-buffered, one barrier per 16-k stage;
-// rows from M up and k from K up read as zero. B goes from memory straight
-// into the MFMA operand registers: wave w owns all 64 rows and columns
-// n0 + 32 w .. + 31, and lane (g, c) feeds MFMA block b (0, 1) with column
-// n0 + 32 w + 2 c + b, so one 16-byte load per k-row gives it both blocks'
-// operand, and B never passes through LDS. MFMA step s of stage t gives lane
-// group g the k index 16 t + 4 g + s, the order of gemm_kernel, whose results
-// it reproduces bitwise. 123-128 VGPRs: four waves per SIMD. NT: B is read
-// once (M <= 64, the AO->MO half transform), so its loads bypass the caches.
-// AO->MO half transform (64 x 786432 x 512) against the LDS-staged small-M
-// tile: 0.877-0.883 against 0.893-0.900 ms on one box and 0.885-0.886 against
-// 0.913-0.915 ms on another, alternating; M < 64 (48 x 65536 x 256, four
-// batches) measured the same.
-template <bool FULLM, bool TA, bool NT>
+// GEMM with B stored [k][n] (row-major): fp64 on 64 x 128 tiles (N a multiple
+// of 128), fp32 on 64 x 256 tiles (N a multiple of 256), four waves each.
+// A (either layout) is staged through LDS one 64-row slab per workgroup,
+// double-buffered, one barrier per 16-k stage; rows from M up and k from K up
+// read as zero. B goes from memory straight into the MFMA operand registers:
+// wave w owns all 64 rows and 16 NB columns (NB = 16 bytes / element: 2 for
+// fp64, 4 for fp32), and lane (g, c) feeds MFMA block b (0 .. NB - 1) with
+// column n0 + 16 NB w + NB c + b, so one 16-byte load per k-row gives it every
+// block's operand and B never passes through LDS. MFMA step s of stage t gives
+// lane group g the k index 16 t + 4 g + s, the order of gemm_kernel, whose
+// results it reproduces bitwise. 118-128 VGPRs: four waves per SIMD. NT: B is
+// read once (M <= 64, e.g. the AO->MO half transform), so its loads bypass the
+// caches. AO->MO half transform (64 x 786432 x 512) against the LDS-staged
+// small-M tile: 0.877-0.883 against 0.893-0.900 ms on one box and 0.885-0.886
+// against 0.913-0.915 ms on another, alternating; M < 64 (48 x 65536 x 256,
+// four batches) measured the same.
+template <typename T, bool FULLM, bool TA, bool NT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_directb_kernel(GemmArgs g) {
-    typedef double T;
     typedef Mfma<T> MF;
-    typedef MF::acc_t acc_t;
-    typedef d2_t v2;
+    typedef typename MF::acc_t acc_t;
+    constexpr int NB = 16 / sizeof(T);  // MFMA column blocks per wave: one 16-byte B piece per lane
+    constexpr int BN = 64 * NB;         // tile columns: 128 (fp64), 256 (fp32)
+    typedef typename VecN<T, NB>::type vb_t;
     typedef Stage<T, 64, !TA, true, kBK> SA;  // A: a 64-row slab, [k][m] (TA) or [m][k] in LDS
     __shared__ __attribute__((aligned(16))) T lds[2 * SA::ELEMS];
 
@@ -421,28 +423,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int64_t nk = (g.K + kBK - 1) / kBK;
     const int64_t nfull = g.K / kBK;
 
-    acc_t acc[4][2];
+    acc_t acc[4][NB];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
+        for (int b = 0; b < NB; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
     if (nk > 0) {
         const int lane = threadIdx.x & 63;
         const int lg = lane >> 4;
         const int c = lane & 15;
-        const T* B = static_cast<const T*>(g.B) + bat * g.sB + tn * 128 + (threadIdx.x >> 6) * 32 + 2 * c +
+        const T* B = static_cast<const T*>(g.B) + bat * g.sB + tn * BN + (threadIdx.x >> 6) * (16 * NB) + NB * c +
                      (int64_t)(4 * lg) * g.ldb;
         SA sa;
-        v2 rb[4];  // B operand of MFMA step s of the current stage
+        vb_t rb[4];  // B operands of MFMA step s of the current stage
         auto bload = [&](int64_t t, int s) __attribute__((always_inline)) {
-            const v2* q = reinterpret_cast<const v2*>(B + (16 * t + s) * g.ldb);
+            const vb_t* q = reinterpret_cast<const vb_t*>(B + (16 * t + s) * g.ldb);
             rb[s] = NT ? __builtin_nontemporal_load(q) : *q;
         };
         // Stage t's B where it may pass K: k-rows from K up read as zero.
         auto bload_tail = [&](int64_t t, int s) __attribute__((always_inline)) {
             const bool ok = 16 * t + 4 * lg + s < g.K;
-            const v2 x = *reinterpret_cast<const v2*>(ok ? B + (16 * t + s) * g.ldb : B - (int64_t)(4 * lg) * g.ldb);
-            rb[s] = ok ? x : v2{0.0, 0.0};
+            const vb_t x = *reinterpret_cast<const vb_t*>(ok ? B + (16 * t + s) * g.ldb : B - (int64_t)(4 * lg) * g.ldb);
+            rb[s] = ok ? x : vb_t{};
         };
         auto aload = [&](int64_t t) __attribute__((always_inline)) {
             if (FULLM && t < nfull) sa.template load<true>(A, g.lda, m0, g.M, t * kBK, g.K);
@@ -456,7 +458,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
-                for (int b = 0; b < 2; ++b) acc[a][b] = MF::mma(fa[a], rb[s][b], acc[a][b]);
+                for (int b = 0; b < NB; ++b) acc[a][b] = MF::mma(fa[a], rb[s][b], acc[a][b]);
         };
         aload(0);
         sa.store(lds);
@@ -470,16 +472,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (; t + 1 < nfull; ++t) {
             // Stage t + 1 of A goes to the other buffer; step s's B operand is
             // reloaded for stage t + 1 as soon as its MFMAs have issued. The
-            // wave issuing the MFMAs runs at raised priority for the burst.
+            // fp64 wave issuing the MFMAs runs at raised priority for the burst.
             aload(t + 1);
             const T* cur = lds + (t & 1) * SA::ELEMS;
-            __builtin_amdgcn_s_setprio(1);
+            if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 step(cur, s);
                 bload(t + 1, s);
             }
-            __builtin_amdgcn_s_setprio(0);
+            if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
             __syncthreads();
@@ -502,31 +504,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int s = 0; s < 4; ++s) step(cur, s);
     }
 
-    // D = alpha * acc (+ beta * C); acc[a][b][r] is row 16 a + lg + 4 r,
-    // column col + b. D and C rows start 16-byte aligned when their leading
-    // dimension is even (checked below), so a lane's two columns are one
-    // 16-byte piece. The lane indices are formed again here rather than held
-    // through the K loop.
+    // D = alpha * acc (+ beta * C); acc[a][b][r] is row m0 + 16 a +
+    // MF::row(lg, r), column col + b. When D's (and C's) rows start 16-byte
+    // aligned (checked below), a lane's NB columns are one 16-byte piece. The
+    // lane indices are formed again here rather than held through the K loop.
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int lg = (tid & 63) >> 4;
-    const int64_t col = tn * 128 + (tid >> 6) * 32 + 2 * (tid & 15);
+    const int64_t col = tn * BN + (tid >> 6) * (16 * NB) + NB * (tid & 15);
     const T alpha = (T)g.alpha;
     const T beta = (T)g.beta;
     const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
     T* D = static_cast<T*>(g.D) + bat * g.sD;
-    const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * 8)) & 15) == 0 &&
-                      (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * 8)) & 15) == 0);
+    const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
+                      (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-        T cv[4][2];
+        T cv[4][NB];
         if (C) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + 16 * a + MF::row(lg, r);
                 const bool ok = FULLM || row < g.M;
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
+                for (int b = 0; b < NB; ++b) {
                     const T x = C[ok ? row * g.ldc + col + b : 0];
                     cv[r][b] = ok ? x : T(0);
                 }
@@ -536,33 +537,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int r = 0; r < 4; ++r) {
             const int64_t row = m0 + 16 * a + MF::row(lg, r);
             if (!FULLM && row >= g.M) continue;
-            T v[2];
+            vb_t v;
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < NB; ++b) {
                 v[b] = acc[a][b][r];
                 if (g.alpha != 1.0) v[b] = alpha * v[b];
                 if (C) v[b] = v[b] + beta * cv[r][b];
             }
             T* d = D + row * g.ldd + col;
             if (vecd) {
-                *reinterpret_cast<v2*>(d) = v2{v[0], v[1]};
+                *reinterpret_cast<vb_t*>(d) = v;
             } else {
-                d[0] = v[0];
-                d[1] = v[1];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) d[b] = v[b];
             }
         }
     }
 }
 
+template <typename T>
 static int launch_directb(GemmArgs& g, bool ta, bool nt, hipStream_t st) {
+    constexpr int BN = 64 * (16 / sizeof(T));
     g.tiles_m = (g.M + 63) / 64;
-    g.tiles_n = g.N / 128;
+    g.tiles_n = g.N / BN;
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const bool full = g.M % 64 == 0;
     const dim3 grid((unsigned)total), block(kThreads);
 #define TT_DIRECTB_CASE(F, A_T, N_T) \
-    if (full == F && ta == A_T && nt == N_T) hipLaunchKernelGGL((gemm_directb_kernel<F, A_T, N_T>), grid, block, 0, st, g);
+    if (full == F && ta == A_T && nt == N_T) hipLaunchKernelGGL((gemm_directb_kernel<T, F, A_T, N_T>), grid, block, 0, st, g);
     TT_DIRECTB_CASE(true, true, true)
     TT_DIRECTB_CASE(false, true, true)
     TT_DIRECTB_CASE(true, true, false)
@@ -631,7 +634,15 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 0.146 ms), so such shapes stay on the LDS-staged tiles.
     if constexpr (sizeof(T) == 8 && !DOT)
         if (!tb && vec && g.N % 128 == 0)
-            return launch_directb(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
+            return launch_directb<T>(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
+    // fp32 on 64 x 256 tiles (four 16-column MFMA blocks per wave, so a lane's
+    // B piece is still 16 bytes): within 1-2% of the LDS-staged tiles, ahead
+    // on short K (same box, alternating, bitwise equal: 4096^2 x 512 0.1345
+    // against 0.1364 ms, 64 x 512^3 with alpha/beta and C 0.1397 against
+    // 0.1414 ms, 4096^3 0.988 against 0.990 ms).
+    if constexpr (sizeof(T) == 4 && !DOT)
+        if (!tb && vec && g.N % 256 == 0)
+            return launch_directb<T>(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
