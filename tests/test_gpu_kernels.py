@@ -162,6 +162,100 @@ def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta
     assert torch.equal(direct, staged)
 
 
+@pytest.mark.parametrize(
+    "ta,M,N,K,batch,alpha,beta,with_c,ldd_pad",
+    [
+        (False, 256, 512, 800, 1, 1.0, 0.0, False, 0),  # NT, the fused config-5 GEMM's shape family
+        (True, 64, 1024, 512, 1, 1.0, 0.0, False, 0),  # TT, M <= 64: non-temporal B loads
+        (False, 50, 256, 37, 2, 1.5, 0.5, True, 1),  # M < 64, K tail, element stores
+        (True, 200, 384, 333, 3, -1.0, 1.0, True, 0),  # ragged M and K, batched
+        (False, 33, 128, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
+        (True, 128, 256, 16, 1, 1.0, 0.25, True, 0),  # one full stage only
+    ],
+)
+def test_gemm_direct_b_k_contiguous_matches_lds_tile(hip, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
+    """fp64 with B stored [n][k] (k-contiguous), N a multiple of 128: the
+    direct-B kernel with 16-byte k pieces. Checked against float64 torch, and
+    bitwise against the LDS-staged tiles (reached with an odd ldb)."""
+    from trntensor_amd.hip import engine
+
+    dt = torch.float64
+    g = torch.Generator().manual_seed(7 * M + N + K + batch + int(ta))
+    dev = torch.device("cuda")
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    lda = a_cols + a_cols % 2
+    ldb_even = K + K % 2
+    ldb_odd = K + 1 if K % 2 == 0 else K
+    A = torch.randn(batch, a_rows, lda, generator=g, dtype=dt)
+    B = torch.randn(batch, N, max(ldb_even, ldb_odd), generator=g, dtype=dt)
+    ld = N + 1 if ldd_pad else N
+    C = torch.randn(batch, M, ld, generator=g, dtype=dt)
+    opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
+    ref = alpha * torch.bmm(opA, B[:, :, :K].transpose(1, 2).contiguous())
+    if with_c:
+        ref = ref + beta * C[:, :, :N]
+    Ad, Cd = A.to(dev), C.to(dev)
+    outs = []
+    for ldb in (ldb_even, ldb_odd):
+        Bd = B[:, :, :ldb].contiguous().to(dev)
+        assert Bd.shape == (batch, N, ldb) and ldb >= K  # rows of K elements, N of them per batch entry
+        D = torch.full((batch, M, ld), float("nan"), dtype=dt, device=dev)
+        engine.gemm(ta, True, M, N, K, Ad, lda, a_rows * lda, Bd, ldb, N * ldb, D, ld, M * ld, batch, alpha, beta,
+                    Cd if with_c else None, ld, M * ld)
+        outs.append(D)
+    torch.cuda.synchronize()
+    direct, staged = outs[0][:, :, :N], outs[1][:, :, :N]
+    assert normwise(direct.cpu(), ref) <= TOL[dt]
+    assert torch.equal(direct, staged)
+
+
+@pytest.mark.parametrize(
+    "ta,tb,M,N,K,batch,with_e2",
+    [
+        (False, True, 256, 512, 800, 1, True),  # the fused config-5 dot GEMM's shape family
+        (False, True, 64, 256, 100, 2, False),  # M = 64: non-temporal B loads
+        (True, False, 128, 384, 37, 3, True),  # K tail, B row-major
+        (True, True, 192, 128, 16, 1, False),
+    ],
+)
+def test_gemm_dot_direct_b_matches_lds_tile(hip, ta, tb, M, N, K, batch, with_e2):
+    """fp64 dot GEMM (sum of op(A) op(B) .* E1 .* E2) with M a multiple of 64 and
+    N of 128: the direct-B kernel's dot epilogue. Against float64 torch, and
+    against the LDS-staged tiles (odd ldb) to 1e-13 relative: the per-tile sums
+    are added in another order."""
+    from trntensor_amd.hip import engine
+
+    dt = torch.float64
+    g = torch.Generator().manual_seed(M + 3 * N + K + batch)
+    dev = torch.device("cuda")
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    lda = a_cols + a_cols % 2
+    ldb_even = b_cols + b_cols % 2
+    ldb_odd = b_cols + 1 if b_cols % 2 == 0 else b_cols
+    A = torch.randn(batch, a_rows, lda, generator=g, dtype=dt)
+    B = torch.randn(batch, b_rows, max(ldb_even, ldb_odd), generator=g, dtype=dt)
+    E1 = torch.randn(batch, M, N, generator=g, dtype=dt)
+    E2 = torch.randn(batch, M, N, generator=g, dtype=dt) if with_e2 else None
+    opA = A[:, :, :a_cols].transpose(1, 2) if ta else A[:, :, :a_cols]
+    opB = B[:, :, :b_cols].transpose(1, 2) if tb else B[:, :, :b_cols]
+    X = torch.bmm(opA.contiguous(), opB.contiguous())
+    ref = float((X * E1 * (E2 if with_e2 else 1.0)).sum())
+    es = [0, N, 0, 1, M * N]  # E[b, m, n]: m_lo extent M, n_lo extent N
+    outs = []
+    for ldb in (ldb_even, ldb_odd):
+        Bd = B[:, :, :ldb].contiguous().to(dev)
+        assert Bd.shape == (batch, b_rows, ldb) and ldb >= b_cols
+        out = torch.zeros(1, dtype=dt, device=dev)
+        engine.gemm_dot(ta, tb, M, N, K, A.to(dev), lda, a_rows * lda, Bd, ldb, b_rows * ldb, batch, M, N, E1.to(dev), es,
+                        E2.to(dev) if with_e2 else None, es if with_e2 else None, 1.0, 0.0, None, out)
+        outs.append(float(out.cpu()))
+    direct, staged = outs
+    scale = float((X.abs() * E1.abs() * (E2.abs() if with_e2 else 1.0)).sum())
+    assert abs(direct - ref) <= 1e-13 * scale
+    assert abs(direct - staged) <= 1e-13 * scale
+
+
 def test_gemm_k_zero_is_beta_c(hip):
     assert _gemm_case(hip, torch.float64, False, False, 9, 11, 0, 2, 1.5, 0.5, True) == 0.0
 

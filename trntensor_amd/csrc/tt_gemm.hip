@@ -385,15 +385,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// GEMM with B stored [k][n] (row-major): fp64 on 64 x 128 tiles (N a multiple
-// of 128), fp32 on 64 x 256 tiles (N a multiple of 256), four waves each.
+// GEMM (or dot epilogue, DOT) with N a multiple of the tile width: fp64 on 64 x
+// 128 tiles, fp32 on 64 x 256 tiles, four waves each.
 // A (either layout) is staged through LDS one 64-row slab per workgroup,
 // double-buffered, one barrier per 16-k stage; rows from M up and k from K up
 // read as zero. B goes from memory straight into the MFMA operand registers:
 // wave w owns all 64 rows and 16 NB columns (NB = 16 bytes / element: 2 for
 // fp64, 4 for fp32), and lane (g, c) feeds MFMA block b (0 .. NB - 1) with
 // column n0 + 16 NB w + NB c + b, so one 16-byte load per k-row gives it every
-// block's operand and B never passes through LDS. MFMA step s of stage t gives
+// block's operand and B never passes through LDS. With B k-contiguous (TB)
+// the lane's 16-byte piece is NB consecutive k of one column instead, and its
+// four pieces cover its NB columns over the stage's 4 k. MFMA step s of stage t gives
 // lane group g the k index 16 t + 4 g + s, the order of gemm_kernel, whose
 // results it reproduces bitwise. 118-128 VGPRs: four waves per SIMD. NT: B is
 // read once (M <= 64, e.g. the AO->MO half transform), so its loads bypass the
@@ -401,13 +403,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 // small-M tile: 0.877-0.883 against 0.893-0.900 ms on one box and 0.885-0.886
 // against 0.913-0.915 ms on another, alternating; M < 64 (48 x 65536 x 256,
 // four batches) measured the same.
-template <typename T, bool FULLM, bool TA, bool NT>
+template <typename T, bool FULLM, bool TA, bool TB, bool NT, bool DOT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_directb_kernel(GemmArgs g) {
     typedef Mfma<T> MF;
     typedef typename MF::acc_t acc_t;
     constexpr int NB = 16 / sizeof(T);  // MFMA column blocks per wave: one 16-byte B piece per lane
     constexpr int BN = 64 * NB;         // tile columns: 128 (fp64), 256 (fp32)
-    typedef typename VecN<T, NB>::type vb_t;
+    constexpr int SPL = TB ? 16 / sizeof(T) : 1;  // MFMA steps one B load feeds (TB: k-contiguous piece)
+    typedef typename VecN<T, 16 / sizeof(T)>::type v16_t;
     typedef Stage<T, 64, !TA, true, kBK> SA;  // A: a 64-row slab, [k][m] (TA) or [m][k] in LDS
     __shared__ __attribute__((aligned(16))) T lds[2 * SA::ELEMS];
 
@@ -432,54 +435,84 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const int lane = threadIdx.x & 63;
         const int lg = lane >> 4;
         const int c = lane & 15;
-        const T* B = static_cast<const T*>(g.B) + bat * g.sB + tn * BN + (threadIdx.x >> 6) * (16 * NB) + NB * c +
-                     (int64_t)(4 * lg) * g.ldb;
-        SA sa;
-        vb_t rb[4];  // B operands of MFMA step s of the current stage
-        auto bload = [&](int64_t t, int s) __attribute__((always_inline)) {
-            const vb_t* q = reinterpret_cast<const vb_t*>(B + (16 * t + s) * g.ldb);
-            rb[s] = NT ? __builtin_nontemporal_load(q) : *q;
+        const int64_t col0 = tn * BN + (threadIdx.x >> 6) * (16 * NB) + NB * c;  // the lane's first column
+        // B row-major: piece p (0..3) is k-row 16 t + 4 g + p, all NB columns.
+        // B k-contiguous: piece p is column col0 + p % NB, k 16 t + 4 g +
+        // SPL (p / NB) .. + SPL - 1 (MFMA steps SPL (p / NB) ..).
+        const T* B = TB ? static_cast<const T*>(g.B) + bat * g.sB + col0 * g.ldb + 4 * lg
+                        : static_cast<const T*>(g.B) + bat * g.sB + col0 + (int64_t)(4 * lg) * g.ldb;
+        auto bptr = [&](int64_t t, int p) __attribute__((always_inline)) -> const T* {
+            return TB ? B + (int64_t)(p % NB) * g.ldb + 16 * t + SPL * (p / NB) : B + (16 * t + p) * g.ldb;
         };
-        // Stage t's B where it may pass K: k-rows from K up read as zero.
-        auto bload_tail = [&](int64_t t, int s) __attribute__((always_inline)) {
-            const bool ok = 16 * t + 4 * lg + s < g.K;
-            const vb_t x = *reinterpret_cast<const vb_t*>(ok ? B + (16 * t + s) * g.ldb : B - (int64_t)(4 * lg) * g.ldb);
-            rb[s] = ok ? x : vb_t{};
+        SA sa;
+        v16_t rb[4];  // B pieces of the current stage
+        auto bload = [&](int64_t t, int p) __attribute__((always_inline)) {
+            const v16_t* q = reinterpret_cast<const v16_t*>(bptr(t, p));
+            rb[p] = NT ? __builtin_nontemporal_load(q) : *q;
+        };
+        // Stage t's B where it may pass K: k from K up reads as zero.
+        auto bload_tail = [&](int64_t t, int p) __attribute__((always_inline)) {
+#pragma unroll
+            for (int e = 0; e < 16 / (int)sizeof(T); ++e) {
+                const int64_t k = 16 * t + 4 * lg + (TB ? SPL * (p / NB) + e : p);
+                const bool ok = k < g.K;
+                const T* q = TB ? bptr(t, p) + e : bptr(t, p) + e;
+                const T x = *(ok ? q : static_cast<const T*>(g.B));
+                rb[p][e] = ok ? x : T(0);
+            }
         };
         auto aload = [&](int64_t t) __attribute__((always_inline)) {
             if (FULLM && t < nfull) sa.template load<true>(A, g.lda, m0, g.M, t * kBK, g.K);
             else sa.template load<false>(A, g.lda, m0, g.M, t * kBK, g.K);
         };
-        auto step = [&](const T* sbuf, int s) __attribute__((always_inline)) {
-            T fa[4];
+        auto afrag = [&](const T* sbuf, int a, int s) __attribute__((always_inline)) -> T {
+            return TA ? sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c] : sbuf[(16 * a + c) * SA::PITCH + 4 * lg + s];
+        };
+        // The MFMAs piece p feeds. Every accumulator still takes MFMA steps
+        // 0, 1, 2, 3 in order.
+        T fa[4][SPL];
+        auto piece = [&](const T* sbuf, int p) __attribute__((always_inline)) {
+            if (!TB) {
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
-                fa[a] = TA ? sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c] : sbuf[(16 * a + c) * SA::PITCH + 4 * lg + s];
+                for (int a = 0; a < 4; ++a) fa[a][0] = afrag(sbuf, a, p);
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+                for (int a = 0; a < 4; ++a)
 #pragma unroll
-                for (int b = 0; b < NB; ++b) acc[a][b] = MF::mma(fa[a], rb[s][b], acc[a][b]);
+                    for (int b = 0; b < NB; ++b) acc[a][b] = MF::mma(fa[a][0], rb[p][b], acc[a][b]);
+            } else {
+                const int h = p / NB, b = p % NB;
+                if (b == 0) {
+#pragma unroll
+                    for (int a = 0; a < 4; ++a)
+#pragma unroll
+                        for (int e = 0; e < SPL; ++e) fa[a][e] = afrag(sbuf, a, SPL * h + e);
+                }
+#pragma unroll
+                for (int e = 0; e < SPL; ++e)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) acc[a][b] = MF::mma(fa[a][e], rb[p][e], acc[a][b]);
+            }
         };
         aload(0);
         sa.store(lds);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            if (nfull > 0) bload(0, s);
-            else bload_tail(0, s);
+        for (int p = 0; p < 4; ++p) {
+            if (nfull > 0) bload(0, p);
+            else bload_tail(0, p);
         }
         __syncthreads();
         int64_t t = 0;
         for (; t + 1 < nfull; ++t) {
-            // Stage t + 1 of A goes to the other buffer; step s's B operand is
-            // reloaded for stage t + 1 as soon as its MFMAs have issued. The
-            // fp64 wave issuing the MFMAs runs at raised priority for the burst.
+            // Stage t + 1 of A goes to the other buffer; B piece p is reloaded
+            // for stage t + 1 as soon as its MFMAs have issued. The fp64 wave
+            // issuing the MFMAs runs at raised priority for the burst.
             aload(t + 1);
             const T* cur = lds + (t & 1) * SA::ELEMS;
             if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                step(cur, s);
-                bload(t + 1, s);
+            for (int p = 0; p < 4; ++p) {
+                piece(cur, p);
+                bload(t + 1, p);
             }
             if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
@@ -491,9 +524,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             aload(t + 1);
             const T* cur = lds + (t & 1) * SA::ELEMS;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                step(cur, s);
-                bload_tail(t + 1, s);
+            for (int p = 0; p < 4; ++p) {
+                piece(cur, p);
+                bload_tail(t + 1, p);
             }
             sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
             __syncthreads();
@@ -501,62 +534,120 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         const T* cur = lds + (t & 1) * SA::ELEMS;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) step(cur, s);
+        for (int p = 0; p < 4; ++p) piece(cur, p);
     }
 
-    // D = alpha * acc (+ beta * C); acc[a][b][r] is row m0 + 16 a +
-    // MF::row(lg, r), column col + b. When D's (and C's) rows start 16-byte
-    // aligned (checked below), a lane's NB columns are one 16-byte piece. The
+    // acc[a][b][r] is row m0 + 16 a + MF::row(lg, r), column col + b. The
     // lane indices are formed again here rather than held through the K loop.
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int lg = (tid & 63) >> 4;
     const int64_t col = tn * BN + (tid >> 6) * (16 * NB) + NB * (tid & 15);
-    const T alpha = (T)g.alpha;
-    const T beta = (T)g.beta;
-    const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
-    T* D = static_cast<T*>(g.D) + bat * g.sD;
-    const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
-                      (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
+    if constexpr (DOT) {
+        // Dot epilogue: sum of D .* E over this tile, one double per
+        // workgroup (see gemm_kernel's), in a fixed order: column blocks,
+        // row blocks, then rows; each block's eight E loads go out together.
+        __shared__ double red[4];
+        const T* E1 = static_cast<const T*>(g.E1) + bat * g.e1s[4];
+        const T* E2 = g.E2 ? static_cast<const T*>(g.E2) + bat * g.e2s[4] : nullptr;
+        double sum = 0.0;
+        // E2 present or not: two straight-line copies of the loop below.
+        auto dot = [&](auto has_e2) __attribute__((always_inline)) {
+            constexpr bool HE2 = decltype(has_e2)::value;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        T cv[4][NB];
-        if (C) {
+            for (int b = 0; b < NB; ++b) {
+                // The row parts below are formed again for every column block
+                // (the empty asm hides that they repeat): held across the
+                // blocks, they would not fit the registers of four waves per
+                // SIMD.
+                int lgb = lg;
+                asm volatile("" : "+v"(lgb));
+                const uint32_t cb = (uint32_t)(col + b);
+                const uint32_t nh = fdiv(cb, g.ndiv);
+                const uint32_t nl = cb - nh * g.ndiv.d;
+                const int64_t o1n = nh * g.e1s[2] + nl * g.e1s[3];
+                const int64_t o2n = nh * g.e2s[2] + nl * g.e2s[3];
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    T e1v[4], e2v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + 16 * a + MF::row(lgb, r);
+                        const bool ok = FULLM || row < g.M;
+                        const uint32_t rr = (uint32_t)(ok ? row : 0);
+                        const uint32_t mh = fdiv(rr, g.mdiv);
+                        const uint32_t ml = rr - mh * g.mdiv.d;
+                        e1v[r] = E1[ok ? mh * g.e1s[0] + ml * g.e1s[1] + o1n : 0];
+                        if (HE2) e2v[r] = E2[ok ? mh * g.e2s[0] + ml * g.e2s[1] + o2n : 0];
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + 16 * a + MF::row(lgb, r);
+                        if (FULLM || row < g.M) {
+                            T e = e1v[r];
+                            if (HE2) e = e * e2v[r];
+                            sum += (double)(acc[a][b][r] * e);
+                        }
+                    }
+                    // One block's loads in flight at a time.
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        if (E2) dot(std::true_type{});
+        else dot(std::false_type{});
+        const double tot = block256_sum(sum, red);
+        if (tid == 0) g.partial[blockIdx.x] = tot;
+        return;
+    } else {
+        // D = alpha * acc (+ beta * C). When D's (and C's) rows start 16-byte
+        // aligned (checked below), a lane's NB columns are one 16-byte piece.
+        const T alpha = (T)g.alpha;
+        const T beta = (T)g.beta;
+        const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
+        T* D = static_cast<T*>(g.D) + bat * g.sD;
+        const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
+                          (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            T cv[4][NB];
+            if (C) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + 16 * a + MF::row(lg, r);
+                    const bool ok = FULLM || row < g.M;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const T x = C[ok ? row * g.ldc + col + b : 0];
+                        cv[r][b] = ok ? x : T(0);
+                    }
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + 16 * a + MF::row(lg, r);
-                const bool ok = FULLM || row < g.M;
+                if (!FULLM && row >= g.M) continue;
+                v16_t v;
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    const T x = C[ok ? row * g.ldc + col + b : 0];
-                    cv[r][b] = ok ? x : T(0);
+                    v[b] = acc[a][b][r];
+                    if (g.alpha != 1.0) v[b] = alpha * v[b];
+                    if (C) v[b] = v[b] + beta * cv[r][b];
                 }
-            }
-        }
+                T* d = D + row * g.ldd + col;
+                if (vecd) {
+                    *reinterpret_cast<v16_t*>(d) = v;
+                } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t row = m0 + 16 * a + MF::row(lg, r);
-            if (!FULLM && row >= g.M) continue;
-            vb_t v;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                v[b] = acc[a][b][r];
-                if (g.alpha != 1.0) v[b] = alpha * v[b];
-                if (C) v[b] = v[b] + beta * cv[r][b];
-            }
-            T* d = D + row * g.ldd + col;
-            if (vecd) {
-                *reinterpret_cast<vb_t*>(d) = v;
-            } else {
-#pragma unroll
-                for (int b = 0; b < NB; ++b) d[b] = v[b];
+                    for (int b = 0; b < NB; ++b) d[b] = v[b];
+                }
             }
         }
     }
 }
 
-template <typename T>
-static int launch_directb(GemmArgs& g, bool ta, bool nt, hipStream_t st) {
+template <typename T, bool DOT>
+static int launch_directb(GemmArgs& g, bool ta, bool tb, bool nt, hipStream_t st) {
     constexpr int BN = 64 * (16 / sizeof(T));
     g.tiles_m = (g.M + 63) / 64;
     g.tiles_n = g.N / BN;
@@ -564,16 +655,17 @@ static int launch_directb(GemmArgs& g, bool ta, bool nt, hipStream_t st) {
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const bool full = g.M % 64 == 0;
     const dim3 grid((unsigned)total), block(kThreads);
-#define TT_DIRECTB_CASE(F, A_T, N_T) \
-    if (full == F && ta == A_T && nt == N_T) hipLaunchKernelGGL((gemm_directb_kernel<T, F, A_T, N_T>), grid, block, 0, st, g);
-    TT_DIRECTB_CASE(true, true, true)
-    TT_DIRECTB_CASE(false, true, true)
-    TT_DIRECTB_CASE(true, true, false)
-    TT_DIRECTB_CASE(false, true, false)
-    TT_DIRECTB_CASE(true, false, true)
-    TT_DIRECTB_CASE(false, false, true)
-    TT_DIRECTB_CASE(true, false, false)
-    TT_DIRECTB_CASE(false, false, false)
+#define TT_DIRECTB_CASE(F, A_T, B_T, N_T)                         \
+    if (full == F && ta == A_T && tb == B_T && nt == N_T)         \
+        hipLaunchKernelGGL((gemm_directb_kernel<T, F, A_T, B_T, N_T, DOT>), grid, block, 0, st, g);
+#define TT_DIRECTB_NT(F, A_T, B_T) TT_DIRECTB_CASE(F, A_T, B_T, true) TT_DIRECTB_CASE(F, A_T, B_T, false)
+#define TT_DIRECTB_TB(F, A_T) TT_DIRECTB_NT(F, A_T, false) TT_DIRECTB_NT(F, A_T, true)
+    TT_DIRECTB_TB(true, true)
+    TT_DIRECTB_TB(false, true)
+    TT_DIRECTB_TB(true, false)
+    TT_DIRECTB_TB(false, false)
+#undef TT_DIRECTB_TB
+#undef TT_DIRECTB_NT
 #undef TT_DIRECTB_CASE
     return check_launch("tt_gemm");
 }
@@ -632,9 +724,16 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // against 0.520 ms. With N % 128 columns left over, a second launch for
     // them ran alone after the first (nocc 50, N = 100002: 0.198 against
     // 0.146 ms), so such shapes stay on the LDS-staged tiles.
-    if constexpr (sizeof(T) == 8 && !DOT)
-        if (!tb && vec && g.N % 128 == 0)
-            return launch_directb<T>(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
+    // B k-contiguous (NT, TT) takes the same kernel, and so does the dot
+    // epilogue when M is a multiple of 64 (with row masking its epilogue
+    // spills). Same box, alternating: 4096^3 NT 2.026 against 2.130 ms and TT
+    // 2.025 against 2.104 ms (bitwise equal); the fused contraction of config
+    // 5 (dot GEMM 160000 x 16384 x 800, B k-contiguous) 66.2-66.4 against
+    // 67.9-68.0 ms, the sum equal to 2e-15 (another order of the per-tile
+    // sums).
+    if constexpr (sizeof(T) == 8)
+        if (vec && g.N % 128 == 0 && (!DOT || g.M % 64 == 0))
+            return launch_directb<T, DOT>(g, ta, tb, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     // fp32 on 64 x 256 tiles (four 16-column MFMA blocks per wave, so a lane's
     // B piece is still 16 bytes): within 1-2% of the LDS-staged tiles, ahead
     // on short K (same box, alternating, bitwise equal: 4096^2 x 512 0.1345
@@ -642,7 +741,7 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 0.1414 ms, 4096^3 0.988 against 0.990 ms).
     if constexpr (sizeof(T) == 4 && !DOT)
         if (!tb && vec && g.N % 256 == 0)
-            return launch_directb<T>(g, ta, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
+            return launch_directb<T, DOT>(g, ta, false, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     if (sizeof(T) == 8 && !DOT && g.M <= 64 && (g.batch == 1 || g.sB != 0))
         return launch_tile<T, 64, 128, 2, 4, DOT, 1, kBK, true>(g, ta, tb, vec, st);
     if (g.M <= 64 || (sizeof(T) == 8 && g.batch > 1 && g.K <= 1024))
