@@ -148,8 +148,6 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     typedef Mfma<T> MF;
     typedef Panel<T, BK, AW> PN;
     constexpr int KS = PN::E;
-    // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS.
-    auto lds = [&](int b, int k) -> T* { return lds_base + (4 * b + k) * PN::ELEMS; };
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wr = (wave >> 1) * 32;
@@ -158,53 +156,94 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // Stages 0 .. nfull-1 are interior (all rows present, all BK k in range).
     const int64_t nfull = (rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
 
+    // DQ (fp64 with Y): each wave's two column fragments (B_j[q] for the X
+    // waves, B_i[q] for the Y waves) go from memory straight into registers: a
+    // lane's fragment is E consecutive k of one row, the same values the LDS
+    // fragment read gives, so energies are bitwise those of staging all four
+    // panels. Only the row panels B_i[p] and B_j[p] pass through LDS, which
+    // halves the LDS stores and cuts the fragment reads per wave from six to
+    // four per stage. A fragment is reloaded for the next stage as soon as its
+    // MFMAs have issued. Config 4 (fp64), same box, alternating: 7.73-7.74
+    // against 7.95-7.98 ms (naux 1199: 7.77 against 8.05 ms). Double-buffering
+    // the two row panels (one barrier per stage, same LDS) measured the same
+    // (7.72-7.77 ms); four waves per SIMD would spill 137 registers.
+    constexpr bool DQ = NEED_Y && sizeof(T) == 8;
+    // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS; with DQ only
+    // panels 0 and 2 are staged, at lds_base + (2 b + k / 2) * ELEMS.
+    auto lds = [&](int b, int k) -> T* { return lds_base + (DQ ? 2 * b + (k >> 1) : 4 * b + k) * PN::ELEMS; };
+    const int qmat = wave >> 1;
+    const int qch = (wave & 1) * 32;
+    const T* qbase = qmat ? base3 : base1;
+    typename PN::vec_t fq[2];
+    auto qload = [&](int b, int64_t k0, auto fast) __attribute__((always_inline)) {
+        constexpr bool F = decltype(fast)::value;
+        const int r = qch + 16 * b + (lane & 15);
+        const int64_t k = k0 + PN::E * (lane >> 4);
+        const T* row = qbase + (int64_t)r * naux;
+#pragma unroll
+        for (int c = 0; c < PN::NP; ++c) {
+            const int64_t gk = k + c * AW;
+            typename PN::piece_t x;
+            if (F || (r < rows_q && gk + AW <= naux)) {
+                x = *reinterpret_cast<const typename PN::piece_t*>(row + gk);
+            } else {
+#pragma unroll
+                for (int e = 0; e < AW; ++e) {
+                    const bool ok = r < rows_q && gk + e < naux;
+                    const T v = *(ok ? row + gk + e : qbase);
+                    x[e] = ok ? v : T(0);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < AW; ++e) fq[b][c * AW + e] = x[e];
+        }
+    };
     PN s0, s1, s2, s3;
     auto load = [&](int64_t k0, auto fast) {
         constexpr bool F = decltype(fast)::value;
         s0.template load<F>(base0, rows_p, naux, k0);
-        s1.template load<F>(base1, rows_q, naux, k0);
+        if (!DQ) s1.template load<F>(base1, rows_q, naux, k0);
         if (NEED_Y) {
             s2.template load<F>(base2, rows_p, naux, k0);
-            s3.template load<F>(base3, rows_q, naux, k0);
+            if (!DQ) s3.template load<F>(base3, rows_q, naux, k0);
         }
     };
     auto store = [&](int buf) {
         s0.store(lds(buf, 0));
-        s1.store(lds(buf, 1));
+        if (!DQ) s1.store(lds(buf, 1));
         if (NEED_Y) {
             s2.store(lds(buf, 2));
-            s3.store(lds(buf, 3));
+            if (!DQ) s3.store(lds(buf, 3));
         }
     };
-    auto compute = [&](int buf) {
-        if (NEED_Y && sizeof(T) == 8) {
+    // next: 0 = no next stage, 1 = interior next stage, 2 = edge next stage
+    // (the column fragments of stage k0n are loaded right after their MFMAs).
+    auto compute = [&](int buf, int64_t k0n, int next) {
+        if (DQ) {
             // fp64: waves 0, 1 form X = P0 P1^T and waves 2, 3 Y = P2 P3^T,
-            // each a 64 x 32 half (columns ch .. ch + 31; row blocks 0, 1 in
-            // X[.][.], 2, 3 in Y[.][.]). A wave reads six fragments per stage
-            // for its 32 MFMAs instead of eight for quadrants of both (166 ->
-            // 158 VGPRs); the epilogue pairs X and Y through LDS. Config 4:
-            // 7.86-7.87 against 7.93 ms, energies bitwise equal. fp32 keeps the
-            // quadrants: split, it needs 104 VGPRs (four workgroups per CU
-            // instead of five) and measured the same (4.145-4.150 against
-            // 4.146-4.158 ms).
-            const int mat = wave >> 1;
-            const int ch = (wave & 1) * 32;
-            const T* rp = lds(buf, mat ? 2 : 0);
-            const T* cp = lds(buf, mat ? 3 : 1);
-            typename PN::vec_t fr[4], fc[2];
+            // each a 64 x 32 half (columns qch .. qch + 31; row blocks 0, 1 in
+            // X[.][.], 2, 3 in Y[.][.]); the epilogue pairs X and Y through
+            // LDS. With all four panels staged, this split read six fragments
+            // per stage for a wave's 32 MFMAs instead of eight for quadrants
+            // of both (166 -> 158 VGPRs; config 4 7.86-7.87 against 7.93 ms).
+            // fp32 keeps the quadrants: split, it needs 104 VGPRs (four
+            // workgroups per CU instead of five) and measured the same.
+            const T* rp = lds(buf, qmat ? 2 : 0);
+            typename PN::vec_t fr[4];
 #pragma unroll
             for (int a = 0; a < 4; ++a) fr[a] = PN::frag(rp, 16 * a, lane);
 #pragma unroll
-            for (int b = 0; b < 2; ++b) fc[b] = PN::frag(cp, ch + 16 * b, lane);
+            for (int b = 0; b < 2; ++b) {
 #pragma unroll
-            for (int st = 0; st < KS; ++st)
+                for (int st = 0; st < KS; ++st)
 #pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        X[a][b] = MF::mma(fr[a][st], fc[b][st], X[a][b]);
-                        Y[a][b] = MF::mma(fr[a + 2][st], fc[b][st], Y[a][b]);
+                    for (int a = 0; a < 2; ++a) {
+                        X[a][b] = MF::mma(fr[a][st], fq[b][st], X[a][b]);
+                        Y[a][b] = MF::mma(fr[a + 2][st], fq[b][st], Y[a][b]);
                     }
+                if (next == 1) qload(b, k0n, std::true_type{});
+                else if (next == 2) qload(b, k0n, std::false_type{});
+            }
             return;
         }
         typename PN::vec_t f0[2], f1[2];
@@ -279,15 +318,20 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
         if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
     };
     if (nk == 0) return;
-    if (nfull > 0) load(0, std::true_type{});
-    else load(0, std::false_type{});
+    if (nfull > 0) {
+        load(0, std::true_type{});
+        if (DQ) qload(0, 0, std::true_type{}), qload(1, 0, std::true_type{});
+    } else {
+        load(0, std::false_type{});
+        if (DQ) qload(0, 0, std::false_type{}), qload(1, 0, std::false_type{});
+    }
     store(0);
     __syncthreads();
     int64_t kt = 0;
     for (; kt + 1 < nfull; ++kt) {
         load((kt + 1) * BK, std::true_type{});
         prio_hi();
-        compute(0);
+        compute(0, (kt + 1) * BK, 1);
         prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
@@ -298,7 +342,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
         const bool more = kt + 1 < nk;
         if (more) load((kt + 1) * BK, std::false_type{});
         prio_hi();
-        compute(0);
+        compute(0, (kt + 1) * BK, more ? 2 : 0);
         prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
