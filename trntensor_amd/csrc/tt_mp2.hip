@@ -156,7 +156,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // Stages 0 .. nfull-1 are interior (all rows present, all BK k in range).
     const int64_t nfull = (rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
 
-    // DQ (fp64 with Y): each wave's two column fragments (B_j[q] for the X
+    // DQ (with Y): each wave's two column fragments (B_j[q] for the X
     // waves, B_i[q] for the Y waves) go from memory straight into registers: a
     // lane's fragment is E consecutive k of one row, the same values the LDS
     // fragment read gives, so energies are bitwise those of staging all four
@@ -166,8 +166,11 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // MFMAs have issued. Config 4 (fp64), same box, alternating: 7.73-7.74
     // against 7.95-7.98 ms (naux 1199: 7.77 against 8.05 ms). Double-buffering
     // the two row panels (one barrier per stage, same LDS) measured the same
-    // (7.72-7.77 ms); four waves per SIMD would spill 137 registers.
-    constexpr bool DQ = NEED_Y && sizeof(T) == 8;
+    // (7.72-7.77 ms); four waves per SIMD would spill 137 registers. fp32
+    // (the same split, 100 VGPRs, four workgroups per CU instead of five with
+    // quadrants): 4.00-4.02 against 4.11-4.12 ms, naux 1199 4.05 against 4.13
+    // ms, energies bitwise equal.
+    constexpr bool DQ = NEED_Y;
     // Stage buffer b, panel k at lds_base + (4 b + k) * ELEMS; with DQ only
     // panels 0 and 2 are staged, at lds_base + (2 b + k / 2) * ELEMS.
     auto lds = [&](int b, int k) -> T* { return lds_base + (DQ ? 2 * b + (k >> 1) : 4 * b + k) * PN::ELEMS; };
@@ -220,14 +223,13 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // (the column fragments of stage k0n are loaded right after their MFMAs).
     auto compute = [&](int buf, int64_t k0n, int next) {
         if (DQ) {
-            // fp64: waves 0, 1 form X = P0 P1^T and waves 2, 3 Y = P2 P3^T,
-            // each a 64 x 32 half (columns qch .. qch + 31; row blocks 0, 1 in
+            // Waves 0, 1 form X = P0 P1^T and waves 2, 3 Y = P2 P3^T, each a
+            // 64 x 32 half (columns qch .. qch + 31; row blocks 0, 1 in
             // X[.][.], 2, 3 in Y[.][.]); the epilogue pairs X and Y through
             // LDS. With all four panels staged, this split read six fragments
             // per stage for a wave's 32 MFMAs instead of eight for quadrants
-            // of both (166 -> 158 VGPRs; config 4 7.86-7.87 against 7.93 ms).
-            // fp32 keeps the quadrants: split, it needs 104 VGPRs (four
-            // workgroups per CU instead of five) and measured the same.
+            // of both (fp64 166 -> 158 VGPRs; config 4 7.86-7.87 against 7.93
+            // ms; fp32 measured the same at 104 VGPRs).
             const T* rp = lds(buf, qmat ? 2 : 0);
             typename PN::vec_t fr[4];
 #pragma unroll
@@ -246,60 +248,18 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
             }
             return;
         }
+        // X only (i = j or p = q): quadrants, both panels through LDS.
         typename PN::vec_t f0[2], f1[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a) f0[a] = PN::frag(lds(buf, 0), wr + 16 * a, lane);
 #pragma unroll
         for (int b = 0; b < 2; ++b) f1[b] = PN::frag(lds(buf, 1), wc + 16 * b, lane);
-        if (NEED_Y) {
-            // fp32: X's fragments and MFMAs, then Y's. Holding half a
-            // stage's fragments brings the kernel from 112 to 96 VGPRs, five
-            // workgroups per CU instead of four: 4.16 against 4.21 ms at
-            // config 4, energies bitwise equal (each accumulator's MFMAs keep
-            // their order). fp64 stays at three workgroups either way (150
-            // VGPRs; the LDS would hold four) and measured no gain.
-            if (sizeof(T) == 4) {
 #pragma unroll
-                for (int st = 0; st < KS; ++st)
+        for (int st = 0; st < KS; ++st)
 #pragma unroll
-                    for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < 2; ++a)
 #pragma unroll
-                        for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
-                typename PN::vec_t f2[2], f3[2];
-#pragma unroll
-                for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
-#pragma unroll
-                for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
-#pragma unroll
-                for (int st = 0; st < KS; ++st)
-#pragma unroll
-                    for (int a = 0; a < 2; ++a)
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
-                return;
-            }
-            typename PN::vec_t f2[2], f3[2];
-#pragma unroll
-            for (int a = 0; a < 2; ++a) f2[a] = PN::frag(lds(buf, 2), wr + 16 * a, lane);
-#pragma unroll
-            for (int b = 0; b < 2; ++b) f3[b] = PN::frag(lds(buf, 3), wc + 16 * b, lane);
-#pragma unroll
-            for (int st = 0; st < KS; ++st)
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
-                        Y[a][b] = MF::mma(f2[a][st], f3[b][st], Y[a][b]);
-                    }
-        } else {
-#pragma unroll
-            for (int st = 0; st < KS; ++st)
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
-        }
+                for (int b = 0; b < 2; ++b) X[a][b] = MF::mma(f0[a][st], f1[b][st], X[a][b]);
     };
 
     // One LDS stage buffer and one register prefetch set: while stage k is
@@ -402,8 +362,8 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     const int lg = lane >> 4;
     // Rows and columns of the quadrant the energy loop below reads from X and Y.
     int rb = wr, cb0 = wc;
-    if (sizeof(T) == 8 && ymode == 0) {
-        // The K loop left each fp64 X wave with X rows 0-63 of its columns
+    if (ymode == 0) {
+        // The K loop left each X wave with X rows 0-63 of its columns
         // and each Y wave with Y rows 0-63 of the same columns. The X wave
         // keeps rows 0-31 and hands rows 32-63 to the Y wave, which keeps its
         // rows 32-63 and hands rows 0-31 back, through LDS (free after the K
