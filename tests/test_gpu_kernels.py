@@ -115,7 +115,9 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
         (True, 50, 1024, 500, 1, 1.0, 0.0, False, 0),  # M < 64, K tail
         (True, 33, 1152, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
         (True, 1, 256, 31, 1, 1.0, 0.0, False, 0),
-        (True, 64, 1030, 48, 1, 1.0, 0.5, True, 0),  # N not a multiple of 128: the LDS-staged tile in both runs
+        (True, 64, 1030, 48, 1, 1.0, 0.5, True, 0),  # fp64: partial last column tile; fp32: LDS-staged in both runs
+        (False, 200, 300, 100, 2, 1.5, 0.5, True, 1),  # fp64: partial last column tile, ragged M
+        (False, 130, 2, 33, 1, 1.0, 0.0, False, 0),  # fp64: one tile of two columns
         # batched, B cached (64-row slabs of A, either layout)
         (False, 512, 512, 512, 4, 1.5, 0.5, True, 0),  # the 64 x 512^3 batch's shape
         (True, 512, 512, 512, 3, 1.0, 0.0, False, 0),
@@ -125,7 +127,7 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
     ],
 )
 def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
-    """B row-major, N a multiple of 128 (fp64) or 256 (fp32): the kernel that
+    """B row-major, N even (fp64) or a multiple of 256 (fp32): the kernel that
     loads B straight into the MFMA registers. Checked against float64 torch,
     and bitwise against the LDS-staged tiles, which the same problem takes when
     B's leading dimension breaks 16-byte alignment (no vector path)."""
@@ -160,6 +162,7 @@ def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta
     direct, staged = outs[0][:, :, :N], outs[1][:, :, :N]
     assert normwise(direct.cpu().double(), ref) <= TOL[dt]
     assert torch.equal(direct, staged)
+    assert torch.isnan(outs[0][:, :, N:]).all()  # nothing stored past column N
 
 
 @pytest.mark.parametrize(
@@ -171,10 +174,12 @@ def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta
         (True, 200, 384, 333, 3, -1.0, 1.0, True, 0),  # ragged M and K, batched
         (False, 33, 128, 7, 2, 0.5, 2.0, True, 1),  # one partial stage only
         (True, 128, 256, 16, 1, 1.0, 0.25, True, 0),  # one full stage only
+        (False, 192, 200, 64, 1, 1.0, 0.0, False, 0),  # partial last column tile
+        (True, 70, 1030, 100, 2, 1.5, 0.5, True, 1),  # partial last column tile, ragged M
     ],
 )
 def test_gemm_direct_b_k_contiguous_matches_lds_tile(hip, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
-    """fp64 with B stored [n][k] (k-contiguous), N a multiple of 128: the
+    """fp64 with B stored [n][k] (k-contiguous), N even: the
     direct-B kernel with 16-byte k pieces. Checked against float64 torch, and
     bitwise against the LDS-staged tiles (reached with an odd ldb)."""
     from trntensor_amd.hip import engine
@@ -207,6 +212,8 @@ def test_gemm_direct_b_k_contiguous_matches_lds_tile(hip, ta, M, N, K, batch, al
     direct, staged = outs[0][:, :, :N], outs[1][:, :, :N]
     assert normwise(direct.cpu(), ref) <= TOL[dt]
     assert torch.equal(direct, staged)
+    if ld > N:
+        assert torch.isnan(outs[0][:, :, N:]).all()  # nothing stored past column N
 
 
 @pytest.mark.parametrize(

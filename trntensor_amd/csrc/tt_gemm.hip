@@ -385,8 +385,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// GEMM (or dot epilogue, DOT) with N a multiple of the tile width: fp64 on 64 x
-// 128 tiles, fp32 on 64 x 256 tiles, four waves each.
+// GEMM (or dot epilogue, DOT): fp64 on 64 x 128 tiles, fp32 on 64 x 256 tiles,
+// four waves each; N a multiple of NB (below), the last column tile may be
+// partial (not with DOT).
 // A (either layout) is staged through LDS one 64-row slab per workgroup,
 // double-buffered, one barrier per 16-k stage; rows from M up and k from K up
 // read as zero. B goes from memory straight into the MFMA operand registers:
@@ -435,7 +436,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const int lane = threadIdx.x & 63;
         const int lg = lane >> 4;
         const int c = lane & 15;
-        const int64_t col0 = tn * BN + (threadIdx.x >> 6) * (16 * NB) + NB * c;  // the lane's first column
+        // The lane's first column, clamped into the matrix: in a last, partial
+        // column tile the lanes past N read column N - NB instead, and their
+        // results are never stored (a column of D depends on that column of B
+        // only).
+        const int64_t col0 = min(tn * BN + (threadIdx.x >> 6) * (16 * NB) + NB * c, g.N - NB);
         // B row-major: piece p (0..3) is k-row 16 t + 4 g + p, all NB columns.
         // B k-contiguous: piece p is column col0 + p % NB, k 16 t + 4 g +
         // SPL (p / NB) .. + SPL - 1 (MFMA steps SPL (p / NB) ..).
@@ -608,6 +613,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         T* D = static_cast<T*>(g.D) + bat * g.sD;
         const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
                           (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
+        const bool colok = col < g.N;  // N is a multiple of NB: all NB columns or none
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             T cv[4][NB];
@@ -615,7 +621,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int64_t row = m0 + 16 * a + MF::row(lg, r);
-                    const bool ok = FULLM || row < g.M;
+                    const bool ok = (FULLM || row < g.M) && colok;
 #pragma unroll
                     for (int b = 0; b < NB; ++b) {
                         const T x = C[ok ? row * g.ldc + col + b : 0];
@@ -626,7 +632,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + 16 * a + MF::row(lg, r);
-                if (!FULLM && row >= g.M) continue;
+                if ((!FULLM && row >= g.M) || !colok) continue;
                 v16_t v;
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
@@ -650,7 +656,7 @@ template <typename T, bool DOT>
 static int launch_directb(GemmArgs& g, bool ta, bool tb, bool nt, hipStream_t st) {
     constexpr int BN = 64 * (16 / sizeof(T));
     g.tiles_m = (g.M + 63) / 64;
-    g.tiles_n = g.N / BN;
+    g.tiles_n = (g.N + BN - 1) / BN;
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const bool full = g.M % 64 == 0;
@@ -723,7 +729,7 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // ms, the AO->MO transform's two GEMMs 0.885 against 0.914 and 0.492
     // against 0.520 ms. With N % 128 columns left over, a second launch for
     // them ran alone after the first (nocc 50, N = 100002: 0.198 against
-    // 0.146 ms), so such shapes stay on the LDS-staged tiles.
+    // 0.146 ms); a partial last tile in the same launch (below) takes 0.144.
     // B k-contiguous (NT, TT) takes the same kernel, and so does the dot
     // epilogue when M is a multiple of 64 (with row masking its epilogue
     // spills). Same box, alternating: 4096^3 NT 2.026 against 2.130 ms and TT
@@ -731,8 +737,15 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 5 (dot GEMM 160000 x 16384 x 800, B k-contiguous) 66.2-66.4 against
     // 67.9-68.0 ms, the sum equal to 2e-15 (another order of the per-tile
     // sums).
+    // Any even N (a last, partial column tile clamps its columns; the dot
+    // epilogue keeps N a multiple of 128). Same box, alternating, bitwise
+    // equal, against the LDS-staged tiles: 3000 x 3000 x 1000 with alpha/beta
+    // 0.331 against 0.438 ms, NT 0.382 against 0.426 ms, 8192 x 200 x 2048
+    // 0.145 against 0.186 ms, config 5's optimal-order GEMM (400 x 128 x 800
+    // x 400) 0.580 against 0.629 ms. The fp32 tile lost on such shapes (3000
+    // x 3000 x 1000 0.221 against 0.212 ms), so fp32 keeps whole tiles.
     if constexpr (sizeof(T) == 8)
-        if (vec && g.N % 128 == 0 && (!DOT || g.M % 64 == 0))
+        if (vec && (DOT ? g.N % 128 == 0 && g.M % 64 == 0 : g.N % 2 == 0))
             return launch_directb<T, DOT>(g, ta, tb, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     // fp32 on 64 x 256 tiles (four 16-column MFMA blocks per wave, so a lane's
     // B piece is still 16 bytes): within 1-2% of the LDS-staged tiles, ahead
