@@ -267,16 +267,11 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     // barrier it replaces stage k. Half the LDS of double buffering buys a
     // third workgroup per CU, whose MFMAs cover the extra barrier. The
     // scheduling barrier keeps the wait for the prefetch behind the MFMAs.
-    // fp64: the wave issuing its stage's MFMAs runs at raised priority, so
-    // co-resident waves in their load/store phase do not delay the MFMA
-    // stream (measured: +5 points of fp64 MFMA utilisation; fp32 loses, so
-    // it keeps the default priority).
-    auto prio_hi = [] {
-        if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
-    };
-    auto prio_lo = [] {
-        if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
-    };
+    // All waves run at the default priority. With all four panels staged,
+    // raising the fp64 wave's priority over its stage's MFMAs gained 5 points
+    // of MFMA utilisation; with the column fragments loaded directly it costs
+    // 0.7% (config 4, same box, alternating: 7.65 against 7.70 ms; fp32 4.10
+    // against 4.00 ms), so neither dtype raises it.
     if (nk == 0) return;
     if (nfull > 0) {
         load(0, std::true_type{});
@@ -290,9 +285,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     int64_t kt = 0;
     for (; kt + 1 < nfull; ++kt) {
         load((kt + 1) * BK, std::true_type{});
-        prio_hi();
         compute(0, (kt + 1) * BK, 1);
-        prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         store(0);
@@ -301,9 +294,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     for (; kt < nk; ++kt) {
         const bool more = kt + 1 < nk;
         if (more) load((kt + 1) * BK, std::false_type{});
-        prio_hi();
         compute(0, (kt + 1) * BK, more ? 2 : 0);
-        prio_lo();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         if (more) store(0);
