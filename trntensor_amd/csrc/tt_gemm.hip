@@ -509,17 +509,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         int64_t t = 0;
         for (; t + 1 < nfull; ++t) {
             // Stage t + 1 of A goes to the other buffer; B piece p is reloaded
-            // for stage t + 1 as soon as its MFMAs have issued. The fp64 wave
-            // issuing the MFMAs runs at raised priority for the burst.
+            // for stage t + 1 as soon as its MFMAs have issued. With B
+            // k-contiguous the fp64 wave issuing the MFMAs runs at raised
+            // priority for the burst (0.4-0.5% faster); with B row-major the
+            // default priority is faster (same box, alternating, bitwise
+            // equal: AO->MO half transform 0.865 against 0.890 ms, 4096^3 1.883
+            // against 1.924 ms, 64 x 512^3 with alpha/beta 0.266 against 0.275
+            // ms, the transform's batched GEMM 0.479 against 0.511 ms).
             aload(t + 1);
             const T* cur = lds + (t & 1) * SA::ELEMS;
-            if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(1);
+            if (sizeof(T) == 8 && TB) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 piece(cur, p);
                 bload(t + 1, p);
             }
-            if (sizeof(T) == 8) __builtin_amdgcn_s_setprio(0);
+            if (sizeof(T) == 8 && TB) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
             __syncthreads();
