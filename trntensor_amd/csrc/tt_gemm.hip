@@ -725,10 +725,10 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // it stays on this tile only. This tile streams B (non-temporal loads), so
     // a B broadcast over the batch (stride 0, re-read per batch entry) takes
     // the two-buffer tile below.
-    // fp64 with B row-major and N a multiple of 128: A through LDS, B straight
-    // into the MFMA registers (gemm_directb_kernel above), non-temporal when
-    // B is read once (M <= 64). Same box, alternating, bitwise equal, against
-    // the LDS-staged tiles below: 4096^3 with alpha/beta 1.952 against 2.082
+    // fp64: A through LDS, B straight into the MFMA registers
+    // (gemm_directb_kernel above), non-temporal when B is read once (M <= 64).
+    // With B row-major and N a multiple of 128, same box, alternating,
+    // bitwise equal, against the LDS-staged tiles below: 4096^3 with alpha/beta 1.952 against 2.082
     // ms (NN 1.944 against 2.069, TN 1.965 against 2.171), 4096^2 x 512 0.258
     // against 0.274 ms, 64 x 512^3 with alpha/beta and C 0.275 against 0.292
     // ms, the AO->MO transform's two GEMMs 0.885 against 0.914 and 0.492
