@@ -51,8 +51,9 @@ def parse():
 
 
 def timed(torch, fn, steps, warmup):
-    """(wall ms/step, mean event ms/step). Events are recorded on torch's
-    current stream, which is the stream the library launches on."""
+    """(wall ms/step, mean event ms/step, median event ms/step). Events are
+    recorded on torch's current stream, which is the stream the library
+    launches on."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -64,8 +65,8 @@ def timed(torch, fn, steps, warmup):
         b.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    ev = statistics.mean(a.elapsed_time(b) for a, b in evs)
-    return wall, ev
+    times = [a.elapsed_time(b) for a, b in evs]
+    return wall, statistics.mean(times), statistics.median(times)
 
 
 def timed_steady(torch, fn, steps, min_warm_s=0.3):
@@ -91,9 +92,9 @@ def timed_steady(torch, fn, steps, min_warm_s=0.3):
 
 def measured_peaks(torch, dev):
     """Rates this device sustains in microbenchmarks: fp64/fp32/bf16 MFMA with no
-    memory traffic (tt_mfma_rate_probe) and a 1 GiB device-to-device copy
-    (bytes read + written). The datasheet peaks assume the maximum clock;
-    these are what the kernels' fractions can also be read against."""
+    memory traffic (tt_mfma_rate_probe) and HBM streams with no arithmetic
+    (tt_hbm_probe). The datasheet peaks assume the maximum clock; these are
+    what the kernels' fractions can also be read against."""
     from trntensor_amd.hip import _lib
 
     lib = _lib.load()
@@ -114,12 +115,39 @@ def measured_peaks(torch, dev):
 
         _, ms = timed_steady(torch, run, 10)
         out[key] = round(flop / (ms * 1e-3) / 1e12, 2)
-    x = torch.ones(1 << 27, dtype=torch.float64, device=dev)
-    y = torch.empty_like(x)
-    _, ms = timed_steady(torch, lambda: y.copy_(x), 10)
-    out["hbm_copy_GBps"] = round(2 * x.numel() * 8 / (ms * 1e-3) / 1e9, 1)
-    del x, y
+    out.update(hbm_probe(torch, dev, lib, st))
     return out
+
+
+def hbm_probe(torch, dev, lib, st, gib=4):
+    """HBM rate from tt_hbm_probe: read-only, write-only and copy streams of
+    `gib` GiB each (16x the 256 MB MALL), 16-byte accesses, non-temporal or
+    through the caches, 1024/2048/4096 workgroups. hbm_GBps is the best of them (bytes read plus
+    bytes written per second); every case is listed under hbm_probe."""
+    from trntensor_amd.hip import _lib
+
+    nbytes = gib << 30
+    src = torch.ones(nbytes // 8, dtype=torch.float64, device=dev)
+    dst = torch.empty_like(src)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    cases = {}
+    for mode, name, moved in ((0, "read", nbytes), (1, "write", nbytes), (2, "copy", 2 * nbytes)):
+        for cached in (0, 4):
+            for wgs in (1024, 2048, 4096):
+                def run(m=mode + cached, wgs=wgs):
+                    _lib.check(lib.tt_hbm_probe(m, src.data_ptr(), dst.data_ptr(), nbytes, wgs, flag.data_ptr(), st),
+                               "tt_hbm_probe")
+
+                _, ms = timed_steady(torch, run, 10, 0.1)
+                cases[f"{name}_{'cached' if cached else 'nt'}_wg{wgs}"] = round(moved / (ms * 1e-3) / 1e9, 1)
+    del src, dst
+    best = max(cases, key=cases.get)
+    return {
+        "hbm_GBps": cases[best],
+        "hbm_method": f"tt_hbm_probe {best} on {gib} GiB buffers, 16-byte accesses, "
+        "median of 10 HIP-event-timed launches",
+        "hbm_probe": cases,
+    }
 
 
 def add_measured_fractions(extra, peaks):
@@ -131,7 +159,7 @@ def add_measured_fractions(extra, peaks):
         "f64": PEAK["f64"] / (peaks["mfma_f64_TFLOPs"] * 1e12),
         "f32": PEAK["f32"] / (peaks["mfma_f32_TFLOPs"] * 1e12),
         "bf16": PEAK["bf16"] / (peaks["mfma_bf16_TFLOPs"] * 1e12),
-        "hbm": PEAK["hbm"] / (peaks["hbm_copy_GBps"] * 1e9),
+        "hbm": PEAK["hbm"] / (peaks["hbm_GBps"] * 1e9),
     }
 
     def dtype_of(name, inherited):
@@ -140,20 +168,29 @@ def add_measured_fractions(extra, peaks):
                 return dt
         return inherited
 
-    def walk(d, dt):
+    over = []
+
+    def put(d, key, value, path):
+        d[key] = round(value, 4)
+        if value > 1.0:
+            over.append(f"{path}.{key}")
+
+    def walk(d, dt, path):
         for k, v in list(d.items()):
             if isinstance(v, dict):
                 if k != "cpu":
-                    walk(v, dtype_of(k, dt))
+                    walk(v, dtype_of(k, dt), f"{path}.{k}" if path else k)
             elif isinstance(v, (int, float)) and not isinstance(v, bool):
                 if k in ("frac_mfma", "frac_binding_roofline", "ao_to_mo_frac_mfma"):
-                    d[k + "_of_measured"] = round(v * ratio[dt], 4)
+                    put(d, k + "_of_measured", v * ratio[dt], path)
                 elif k == "frac_mfma_f32":
-                    d[k + "_of_measured"] = round(v * ratio["f32"], 4)
+                    put(d, k + "_of_measured", v * ratio["f32"], path)
                 elif k == "frac_hbm":
-                    d[k + "_of_measured"] = round(v * ratio["hbm"], 4)
+                    put(d, k + "_of_measured", v * ratio["hbm"], path)
 
-    walk(extra, "f64")
+    walk(extra, "f64", "")
+    # A fraction above 1 means the probe did not find the device's peak.
+    return over
 
 
 def host_info(torch):
@@ -179,18 +216,47 @@ def mp2_inputs(torch, dtype, nocc=64, nvir=320, naux=1200):
     return B.to(dtype), eo.to(dtype), ev.to(dtype)
 
 
-def traffic_from_profiles(kernel_key):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+TRAFFIC_FILE = "profiles/traffic.json"
+PROFILE_FILE = "profiles/headline_profile.json"
+# Sustained-clock spread between boxes of the pool under a long MFMA-bound
+# load, as a fraction of the kernel time: the same build's headline measured
+# 7.49-8.23 ms on different boxes while the MFMA-only probe read 77.3-78.0
+# TFLOP/s on all of them.
+BOX_SPREAD = 0.10
+
+
+def _profiles_json(rel):
     try:
-        with open(path) as f:
-            return json.load(f).get(kernel_key)
+        with open(os.path.join(ROOT, rel)) as f:
+            return json.load(f)
     except (OSError, ValueError):
+        return {}
+
+
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if
+    present. Not measured in this run: copied from TRAFFIC_FILE."""
+    return _profiles_json(TRAFFIC_FILE).get(kernel_key)
+
+
+def profile_from_profiles(kernel_key, frac):
+    """The committed rocprofv3 kernel-trace figures of the headline kernel
+    (PROFILE_FILE: median and mean dispatch time and the fraction they give,
+    the summary file, and the bench line printed in that same profiled run),
+    with how far this run's fraction lies from the profile's."""
+    rec = _profiles_json(PROFILE_FILE).get(kernel_key)
+    if not rec:
         return None
+    out = dict(rec)
+    out["this_run_vs_profile"] = round(frac / rec["frac"] - 1.0, 4)
+    out["within_box_spread"] = abs(frac / rec["frac"] - 1.0) <= BOX_SPREAD
+    return out
 
 
 def cpu_threads(torch):
-    threads = min(16, os.cpu_count() or 1)
+    """Every host core for the CPU baseline (torch.set_num_threads(os.cpu_count()));
+    returns the count used."""
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     return threads
 
@@ -217,8 +283,7 @@ def cpu_mp2_baseline(torch, seconds=12.0):
     (algorithmic GFLOP/s over the i<=j work)."""
     from oracle import cpu_ref
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    threads = cpu_threads(torch)
     B, eo, ev = mp2_inputs(torch, torch.float64)
     nocc = B.shape[0]
     pairs = [(i, j) for i in range(nocc) for j in range(nocc)]
@@ -292,9 +357,10 @@ def main():
     flop = 2080 * 2 * 320**2 * 1200
     print("bench: mp2_energy fp64 64x320x1200", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
-    wall, ev_ms = timed(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps, args.warmup)
+    wall, ev_ms, ev_med = timed(torch, lambda: tt.mp2_energy(B, eo, ev), args.steps, args.warmup)
     value = flop / (wall * 1e-3) / 1e9
     achieved = flop / (ev_ms * 1e-3)
+    kernel_key = "mp2_energy_kernel<double>"
     line = {
         "metric": "DF-MP2 energy GFLOP/s + % fp64 MFMA peak; AO->MO GB/s, 1 MI355X",
         "value": round(value, 1),
@@ -320,7 +386,8 @@ def main():
             "peak": 78.6,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK["f64"], 4),
-            "traffic": traffic_from_profiles("mp2_energy_kernel<double>"),
+            "traffic": traffic_from_profiles(kernel_key),
+            "traffic_source": TRAFFIC_FILE + " (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated; not this run)",
             # The byte counters see every L2 miss; the DRAM-request counter
             # (TCC_EA0_RDREQ_DRAM) reads the same 33 GB, so MALL hits are
             # included. B (197 MB) fits the 256 MB MALL: the panel re-reads of
@@ -328,6 +395,10 @@ def main():
             "traffic_scope": "L2 misses (MALL hits + HBM); B fits the 256 MB MALL",
             "algorithmic_bytes": int(B.numel() * B.element_size() + (eo.numel() + ev.numel()) * 8),
             "event_ms_per_launch": round(ev_ms, 4),
+            "event_ms_median": round(ev_med, 4),
+            "frac_at_median": round(flop / (ev_med * 1e-3) / PEAK["f64"], 4),
+            "box_spread": BOX_SPREAD,
+            "profile": profile_from_profiles(kernel_key, achieved / PEAK["f64"]),
         },
     }
     del B, eo, ev
@@ -356,7 +427,7 @@ def main():
             extra["f1_ao_to_mo_full_then_mp2_fp64"] = bench_f1(torch, tt, dev, args)
         if "a5" in want:
             extra["a5_strided_patterns"] = bench_a5(torch, tt, dev, args)
-        add_measured_fractions(extra, peaks)
+        line["measured_peaks"]["fractions_above_1"] = add_measured_fractions(extra, peaks)
         line["configs"] = extra
 
     if not args.no_cpu:
@@ -636,6 +707,13 @@ def bench_c1(torch, tt, dev, args):
     t_graph = per_call(synced(graph.replay), 50)
     res["device_einsum_loop_ms"] = round(t_dev * 1e3, 3)
     res["device_einsum_loop_graph_replay_ms"] = round(t_graph * 1e3, 3)
+    # The reference's residency test (tests/test_nki_kernels.py): five 2048^2
+    # fp32 products on host operands against the same on device-resident ones.
+    Ah, Bh = torch.randn(2048, 2048, generator=g), torch.randn(2048, 2048, generator=g)
+    Ad, Bdd = Ah.to(dev), Bh.to(dev)
+    t_cold = per_call(lambda: tt.einsum("ij,jk->ik", Ah, Bh), 5, 0.1)
+    t_hot = per_call(synced(lambda: tt.einsum("ij,jk->ik", Ad, Bdd)), 5, 0.1)
+    res["residency_speedup_2048"] = round(t_cold / t_hot, 2)
     if not args.no_cpu:
         from oracle import cpu_ref
 

@@ -11,7 +11,10 @@
  * Conventions (all entry points):
  *  - Plain pointers and sizes only. Every pointer named "device" is device
  *    memory on the current HIP device; the library never allocates or frees
- *    memory and keeps no mutable global state, so calls are re-entrant.
+ *    memory. Every entry point except tt_mp2_energy_noalloc keeps no mutable
+ *    global state, so those calls are re-entrant; tt_mp2_energy_noalloc
+ *    works in a per-device static array, so its calls that overlap on one
+ *    device race (see its declaration).
  *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
  *    Work is enqueued on it and the call returns without synchronising.
  *  - dtype codes: TT_F32 = 0 (float), TT_F64 = 1 (double). TT_F64_DD = 2
@@ -38,7 +41,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 3
+#define TT_ABI_VERSION 4
 #define TT_MAX_DIMS 8
 
 enum { TT_OK = 0, TT_INVALID = 1, TT_UNSUPPORTED = 2, TT_HIP_ERROR = 3 };
@@ -175,7 +178,11 @@ int tt_mp2_energy_shard(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
  * the process ends. A deterministic problem needing more returns TT_INVALID.
  * The call allocates nothing. Every call on one device shares that array,
  * so calls that overlap on one device (different streams, or threads) race;
- * calls ordered on one stream do not.
+ * calls ordered on one stream do not. The first call on each device looks
+ * up the array's device address (a runtime call, not a stream operation),
+ * so it must be made outside stream capture: a first call while `stream`
+ * is capturing returns TT_INVALID. Make one eager call on each device before
+ * capturing; later calls record only kernel launches.
  */
 int tt_mp2_energy_noalloc(int dtype, int64_t nocc, int64_t nvir, int64_t naux,
                           const void* B, const void* eps_occ, const void* eps_vir,
@@ -245,6 +252,22 @@ int tt_strided_contract(int dtype, int n_out, const int64_t* out_shape,
  * peak that the benchmark reports next to the datasheet peak.
  */
 int tt_mfma_rate_probe(int dtype, int64_t workgroups, int64_t iters, void* out, void* stream);
+
+/*
+ * Measurement aid with no counterpart in the reference: streams `bytes`
+ * (a multiple of 16) through HBM with 16-byte accesses from `workgroups`
+ * workgroups of 256 threads, grid-stride. mode 0 reads src (device; `flag`,
+ * one device uint32, is written only if the data's XOR equals a fixed word,
+ * so the loads cannot be dropped), mode 1 writes dst, mode 2 copies src to
+ * dst (the two must not overlap). Modes 0-2 use non-temporal accesses;
+ * modes 4-6 are the same through the caches. src and dst 16-byte aligned.
+ * Timing it on
+ * buffers well beyond the 256 MB MALL gives the HBM rate the device
+ * sustains, the measured peak the benchmark reports beside the 8 TB/s
+ * datasheet figure.
+ */
+int tt_hbm_probe(int mode, const void* src, void* dst, int64_t bytes, int64_t workgroups, void* flag,
+                 void* stream);
 
 #ifdef __cplusplus
 }

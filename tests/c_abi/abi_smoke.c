@@ -46,6 +46,9 @@ int main(void) {
     expect(tt_strided_contract(TT_I64, 1, shape, shape, shape, 0, shape, shape, shape, dummy, NULL, 0.5, 0.0, NULL, dummy,
                                NULL, 0, NULL),
            TT_INVALID, "int64 with a fractional alpha");
+    expect(tt_hbm_probe(7, dummy, dummy, 64, 1, dummy, NULL), TT_INVALID, "hbm probe mode");
+    expect(tt_hbm_probe(0, dummy, dummy, 24, 1, dummy, NULL), TT_INVALID, "hbm probe bytes not a multiple of 16");
+    expect(tt_hbm_probe(0, NULL, dummy, 64, 1, dummy, NULL), TT_INVALID, "hbm probe read without src");
     if (fails == 0) printf("c abi ok\n");
     return fails ? 1 : 0;
 }

@@ -79,3 +79,43 @@ def test_force_backend_env(monkeypatch):
     monkeypatch.delenv("TRNTENSOR_FORCE_BACKEND")
     trntensor.set_backend("pytorch")
     assert dispatch._use_hip() is False
+
+
+class _FakeMp2Lib:
+    """tt_mp2_energy_workspace_bytes with the library's sizes: partials for
+    the work units plus, for naux off a multiple of 16, the padded copy."""
+
+    def tt_mp2_energy_workspace_bytes(self, code, nocc, nvir, naux):
+        part = 8 * (nocc * (nocc + 1) // 2 * 3 + 1)
+        pad = 0 if naux % 16 == 0 else nocc * nvir * ((naux + 15) // 16 * 16) * 8
+        return part + pad
+
+
+def test_mp2_workspace_falls_back_to_partials_on_oom():
+    """An unaligned naux asks for the padded copy first; when the device cannot
+    hold it (OutOfMemoryError), the call gets the partials-only workspace, with
+    which the library runs on B as given."""
+    lib = _FakeMp2Lib()
+    asked = []
+
+    def alloc_oom_above(limit):
+        def alloc(n):
+            asked.append(n)
+            if n > limit:
+                raise torch.OutOfMemoryError("no room for the padded copy")
+            return torch.empty(n, dtype=torch.uint8)
+
+        return alloc
+
+    full = lib.tt_mp2_energy_workspace_bytes(1, 4, 100, 1199)
+    part = lib.tt_mp2_energy_workspace_bytes(1, 4, 100, 1200)
+    assert full > part
+    ws, nb = dispatch._mp2_workspace(lib, 1, 4, 100, 1199, None, _alloc=alloc_oom_above(part))
+    assert nb == part and ws.numel() == part and asked == [full, part]
+    asked.clear()
+    ws, nb = dispatch._mp2_workspace(lib, 1, 4, 100, 1199, None, _alloc=alloc_oom_above(full))
+    assert nb == full and ws.numel() == full and asked == [full]
+    asked.clear()
+    # naux a multiple of 16: no copy is asked for.
+    ws, nb = dispatch._mp2_workspace(lib, 1, 4, 100, 1200, None, _alloc=alloc_oom_above(full))
+    assert nb == part and asked == [part]

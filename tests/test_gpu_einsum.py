@@ -624,3 +624,27 @@ class TestIntegerAndComplex:
         ref = cpu_ref.einsum("ij,jk->ik", A.conj(), B)
         got = trntensor.einsum("ij,jk->ik", A.cuda().conj(), B.cuda())
         assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= 1e-12
+
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_real_operands_complex_scalars(self, hip, dt):
+        """A complex alpha makes a real result complex (result.mul(alpha));
+        a complex beta with a real result and out raises torch's error, and is
+        accepted when out or alpha makes the sum complex."""
+        g = torch.Generator().manual_seed(11)
+        A = torch.randn(24, 40, generator=g, dtype=torch.float64).to(dt)
+        B = torch.randn(40, 16, generator=g, dtype=torch.float64).to(dt)
+        outr = torch.randn(24, 16, generator=g, dtype=torch.float64).to(dt)
+        bar = 1e-12 if dt == torch.float64 else 1e-5
+        for kw in ({"alpha": 2j}, {"alpha": 1.5 - 0.5j, "beta": 0.5, "out": outr}, {"alpha": 2j, "beta": 1j, "out": outr},
+                   {"alpha": 1 + 0j}, {"beta": 2j}):
+            ref = cpu_ref.einsum("ij,jk->ik", A, B, **kw)
+            got = trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), **{k: (v.cuda() if torch.is_tensor(v) else v) for k, v in kw.items()})
+            assert got.dtype == ref.dtype and got.shape == ref.shape, kw
+            if ref.dtype.is_complex:
+                assert normwise(torch.view_as_real(got.cpu()), torch.view_as_real(ref)) <= bar, kw
+            else:
+                assert normwise(got.cpu(), ref) <= bar, kw
+        with pytest.raises(RuntimeError, match="complex"):
+            cpu_ref.einsum("ij,jk->ik", A, B, beta=1j, out=outr)
+        with pytest.raises(RuntimeError, match="complex"):
+            trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), beta=1j, out=outr.cuda())

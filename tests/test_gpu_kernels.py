@@ -396,3 +396,43 @@ def test_mfma_rate_probe_closed_form(hip, code, dt, expected_per_iter, tol):
         _lib.check(lib.tt_mfma_rate_probe(code, 0, 1, out.data_ptr(), st), "tt_mfma_rate_probe")
     with pytest.raises(NotImplementedError):
         _lib.check(lib.tt_mfma_rate_probe(2, 1, 1, out.data_ptr(), st), "tt_mfma_rate_probe")
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("M,ntiles,K,batch,alpha", [
+    (64, 3104, 512, 1, 1.0),           # the AO->MO half transform's shape class (B streamed, M <= 64)
+    (64, 3100, 16, 1, 1.5),            # one k-stage per tile
+    (128, 3120, 48, 1, 1.0),           # two row tiles per column tile
+    (192, 3120, 64, 8, -0.5),          # batched, three row tiles: tiles cross batch entries
+])
+def test_gemm_persistent_matches_per_tile_kernel(hip, dt, M, ntiles, K, batch, alpha):
+    """A transposed, B row-major, no C, three or more rounds of 64-row tiles:
+    the persistent direct-B kernel (each workgroup walks a list of tiles, the
+    next tile's first stage loaded during the current tile's last MFMAs).
+    Bitwise equal to the per-tile direct-B kernel, which the same columns take
+    in a launch of fewer tiles (the two keep one MFMA order per output), and
+    checked against float64 torch on sampled columns."""
+    from trntensor_amd.hip import engine
+
+    dev = torch.device("cuda")
+    BN = 128 if dt == torch.float64 else 256
+    nb = ntiles // ((M // 64) * batch)  # column tiles per batch entry
+    N = nb * BN
+    assert (M // 64) * nb * batch >= 3 * 1024  # three rounds on a 256-CU device
+    g = torch.Generator(device=dev).manual_seed(M + K + batch)
+    A = torch.randn(batch, K, M, generator=g, device=dev, dtype=torch.float64).to(dt)  # stored [k][m]
+    B = torch.randn(batch, K, N, generator=g, device=dev, dtype=torch.float64).to(dt)
+    D = torch.full((batch, M, N), float("nan"), dtype=dt, device=dev)
+    engine.gemm(True, False, M, N, K, A, M, K * M, B, N, K * N, D, N, M * N, batch, alpha)
+    # The same columns in launches of 16 column tiles (per-tile kernel),
+    # reading B and writing D in place through offsets (ldb = ldd = N).
+    P = torch.full_like(D, float("nan"))
+    for c0 in list(range(0, min(N, 4 * 16 * BN), 16 * BN)) + [N - 16 * BN]:
+        engine.gemm(True, False, M, 16 * BN, K, A, M, K * M, B, N, K * N, P, N, M * N, batch, alpha,
+                    b_off=c0, d_off=c0)
+    torch.cuda.synchronize()
+    cols = torch.cat([torch.arange(0, min(N, 4 * 16 * BN)), torch.arange(N - 16 * BN, N)]).to(dev)
+    assert torch.equal(D[:, :, cols], P[:, :, cols])
+    ref = alpha * torch.bmm(A[:, :, :].transpose(1, 2).double().cpu(), B[:, :, cols].double().cpu())
+    assert normwise(D[:, :, cols].cpu(), ref) <= TOL[dt]
+    assert not torch.isnan(D).any()

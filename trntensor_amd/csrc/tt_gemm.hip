@@ -385,6 +385,81 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// Store epilogue of the direct-B kernels: D = alpha * acc (+ beta * C) for
+// the 64 x BN tile at rows m0.., column tile tn of batch entry bat.
+// acc[a][b][r] is row m0 + 16 a + MF::row(lg, r), column col + b. When D's
+// (and C's) rows start 16-byte aligned (checked below), a lane's NB columns
+// are one 16-byte piece. The lane indices are formed again here rather than
+// held through the K loop.
+// PLAIN: no C, D's rows 16-byte aligned and the tile inside N (the caller
+// checked), so every row is one unconditional 16-byte store per lane.
+template <typename T, bool FULLM, bool PLAIN = false>
+__device__ __forceinline__ void directb_store(const GemmArgs& g, typename Mfma<T>::acc_t (&acc)[4][16 / sizeof(T)],
+                                              int64_t bat, int64_t m0, int64_t tn) {
+    typedef Mfma<T> MF;
+    constexpr int NB = 16 / sizeof(T);
+    constexpr int BN = 64 * NB;
+    typedef typename VecN<T, 16 / sizeof(T)>::type v16_t;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lg = (tid & 63) >> 4;
+    const int64_t col = tn * BN + (tid >> 6) * (16 * NB) + NB * (tid & 15);
+    const T alpha = (T)g.alpha;
+    const T beta = (T)g.beta;
+    T* D = static_cast<T*>(g.D) + bat * g.sD;
+    if constexpr (PLAIN) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v16_t v;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) v[b] = g.alpha != 1.0 ? alpha * acc[a][b][r] : acc[a][b][r];
+                *reinterpret_cast<v16_t*>(D + (m0 + 16 * a + MF::row(lg, r)) * g.ldd + col) = v;
+            }
+        return;
+    }
+    const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
+    const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
+                      (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
+    const bool colok = col < g.N;  // N is a multiple of NB: all NB columns or none
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        T cv[4][NB];
+        if (C) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + 16 * a + MF::row(lg, r);
+                const bool ok = (FULLM || row < g.M) && colok;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const T x = C[ok ? row * g.ldc + col + b : 0];
+                    cv[r][b] = ok ? x : T(0);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + 16 * a + MF::row(lg, r);
+            if ((!FULLM && row >= g.M) || !colok) continue;
+            v16_t v;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                v[b] = acc[a][b][r];
+                if (g.alpha != 1.0) v[b] = alpha * v[b];
+                if (C) v[b] = v[b] + beta * cv[r][b];
+            }
+            T* d = D + row * g.ldd + col;
+            if (vecd) {
+                *reinterpret_cast<v16_t*>(d) = v;
+            } else {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) d[b] = v[b];
+            }
+        }
+    }
+}
+
 // GEMM (or dot epilogue, DOT): fp64 on 64 x 128 tiles, fp32 on 64 x 256 tiles,
 // four waves each; N a multiple of NB (below), the last column tile may be
 // partial (not with DOT).
@@ -547,13 +622,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int p = 0; p < 4; ++p) piece(cur, p);
     }
 
-    // acc[a][b][r] is row m0 + 16 a + MF::row(lg, r), column col + b. The
-    // lane indices are formed again here rather than held through the K loop.
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const int lg = (tid & 63) >> 4;
-    const int64_t col = tn * BN + (tid >> 6) * (16 * NB) + NB * (tid & 15);
     if constexpr (DOT) {
+        // acc[a][b][r] is row m0 + 16 a + MF::row(lg, r), column col + b. The
+        // lane indices are formed again here rather than held through the K
+        // loop.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lg = (tid & 63) >> 4;
+        const int64_t col = tn * BN + (tid >> 6) * (16 * NB) + NB * (tid & 15);
         // Dot epilogue: sum of D .* E over this tile, one double per
         // workgroup (see gemm_kernel's), in a fixed order: column blocks,
         // row blocks, then rows; each block's eight E loads go out together.
@@ -610,51 +686,155 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (tid == 0) g.partial[blockIdx.x] = tot;
         return;
     } else {
-        // D = alpha * acc (+ beta * C). When D's (and C's) rows start 16-byte
-        // aligned (checked below), a lane's NB columns are one 16-byte piece.
-        const T alpha = (T)g.alpha;
-        const T beta = (T)g.beta;
-        const T* C = g.C ? static_cast<const T*>(g.C) + bat * g.sC : nullptr;
-        T* D = static_cast<T*>(g.D) + bat * g.sD;
-        const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
-                          (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
-        const bool colok = col < g.N;  // N is a multiple of NB: all NB columns or none
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            T cv[4][NB];
-            if (C) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t row = m0 + 16 * a + MF::row(lg, r);
-                    const bool ok = (FULLM || row < g.M) && colok;
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const T x = C[ok ? row * g.ldc + col + b : 0];
-                        cv[r][b] = ok ? x : T(0);
-                    }
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = m0 + 16 * a + MF::row(lg, r);
-                if ((!FULLM && row >= g.M) || !colok) continue;
-                v16_t v;
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    v[b] = acc[a][b][r];
-                    if (g.alpha != 1.0) v[b] = alpha * v[b];
-                    if (C) v[b] = v[b] + beta * cv[r][b];
-                }
-                T* d = D + row * g.ldd + col;
-                if (vecd) {
-                    *reinterpret_cast<v16_t*>(d) = v;
-                } else {
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) d[b] = v[b];
-                }
-            }
-        }
+        directb_store<T, FULLM>(g, acc, bat, m0, tn);
     }
+}
+
+// Persistent form of gemm_directb_kernel (store epilogue, no C, D 16-byte
+// aligned, whole 64-row and BN-column tiles, K a positive multiple of 16): each workgroup walks a list of tiles
+// and the stages of consecutive tiles form one software pipeline. The next
+// tile's first stage (A slab into LDS, B pieces into registers) is loaded
+// during the current tile's last MFMAs, and the current tile's stores are
+// issued while those loads are in flight, so no workgroup waits out a
+// memory latency between tiles. Hardware workgroup w runs on XCD w % 8; the
+// tiles are split into eight contiguous ranges, one per XCD, and the
+// workgroups of an XCD take that range's tiles round-robin. The MFMA order
+// per accumulator is gemm_directb_kernel's: results are bitwise equal.
+template <typename T, bool TA, bool TB, bool NT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemm_directb_persistent_kernel(
+    GemmArgs g) {
+    typedef Mfma<T> MF;
+    typedef typename MF::acc_t acc_t;
+    constexpr int NB = 16 / sizeof(T);
+    constexpr int BN = 64 * NB;
+    constexpr int SPL = TB ? 16 / sizeof(T) : 1;
+    typedef typename VecN<T, 16 / sizeof(T)>::type v16_t;
+    typedef Stage<T, 64, !TA, true, kBK> SA;
+    __shared__ __attribute__((aligned(16))) T lds[2 * SA::ELEMS];
+
+    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t total = tiles * g.batch;
+    const int64_t x = blockIdx.x % kNumXcd;
+    const int64_t per = gridDim.x / kNumXcd;  // the grid is a multiple of 8
+    const int64_t hi = total * (x + 1) / kNumXcd;
+    int64_t id = total * x / kNumXcd + blockIdx.x / kNumXcd;
+    if (id >= hi) return;  // the whole workgroup: no barrier is left waiting
+    const int64_t nk = g.K / kBK;
+
+    const int lane = threadIdx.x & 63;
+    const int lg = lane >> 4;
+    const int c = lane & 15;
+    // The lane's offset into a tile's B panel (N is a multiple of BN: no
+    // column clamp), the same for every tile; the tile bases are uniform.
+    const int64_t wcol = (threadIdx.x >> 6) * (16 * NB) + NB * c;
+    const int64_t boff = TB ? wcol * g.ldb + 4 * lg : wcol + (int64_t)(4 * lg) * g.ldb;
+    struct Tile {
+        const T* A;
+        const T* B;
+        int64_t bat, tn, m0;
+    };
+    auto tile = [&](int64_t tid) __attribute__((always_inline)) -> Tile {
+        Tile u;
+        u.bat = tid / tiles;
+        const int64_t rem = tid - u.bat * tiles;
+        u.tn = rem / g.tiles_m;
+        u.m0 = (rem - u.tn * g.tiles_m) * 64;
+        u.A = static_cast<const T*>(g.A) + u.bat * g.sA;
+        u.B = static_cast<const T*>(g.B) + u.bat * g.sB + (TB ? u.tn * BN * g.ldb : u.tn * BN);
+        return u;
+    };
+    SA sa;
+    v16_t rb[4];
+    auto bload = [&](const T* B, int64_t t, int p) __attribute__((always_inline)) {
+        const T* q = (TB ? B + (int64_t)(p % NB) * g.ldb + 16 * t + SPL * (p / NB) : B + (16 * t + p) * g.ldb) + boff;
+        rb[p] = NT ? __builtin_nontemporal_load(reinterpret_cast<const v16_t*>(q)) : *reinterpret_cast<const v16_t*>(q);
+    };
+    auto afrag = [&](const T* sbuf, int a, int s) __attribute__((always_inline)) -> T {
+        return TA ? sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c] : sbuf[(16 * a + c) * SA::PITCH + 4 * lg + s];
+    };
+    acc_t acc[4][NB];
+    T fa[4][SPL];
+    auto piece = [&](const T* sbuf, int p) __attribute__((always_inline)) {
+        if (!TB) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fa[a][0] = afrag(sbuf, a, p);
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[a][b] = MF::mma(fa[a][0], rb[p][b], acc[a][b]);
+        } else {
+            const int h = p / NB, b = p % NB;
+            if (b == 0) {
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int e = 0; e < SPL; ++e) fa[a][e] = afrag(sbuf, a, SPL * h + e);
+            }
+#pragma unroll
+            for (int e = 0; e < SPL; ++e)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) acc[a][b] = MF::mma(fa[a][e], rb[p][e], acc[a][b]);
+        }
+    };
+
+    Tile cur = tile(id);
+    sa.template load<true>(cur.A, g.lda, cur.m0, g.M, 0, g.K);
+    sa.store(lds);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) bload(cur.B, 0, p);
+    __syncthreads();
+    int buf = 0;
+    for (;;) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
+        for (int64_t t = 0; t + 1 < nk; ++t) {
+            sa.template load<true>(cur.A, g.lda, cur.m0, g.M, (t + 1) * kBK, g.K);
+            const T* sb = lds + buf * SA::ELEMS;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                piece(sb, p);
+                bload(cur.B, t + 1, p);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            sa.store(lds + (buf ^ 1) * SA::ELEMS);
+            __syncthreads();
+            buf ^= 1;
+        }
+        // Last stage: the next tile's first stage goes out behind its MFMAs.
+        const int64_t nid = id + per;
+        const bool more = nid < hi;
+        const Tile nxt = tile(more ? nid : id);
+        if (more) sa.template load<true>(nxt.A, g.lda, nxt.m0, g.M, 0, g.K);
+        const T* sb = lds + buf * SA::ELEMS;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            piece(sb, p);
+            if (more) bload(nxt.B, 0, p);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) sa.store(lds + (buf ^ 1) * SA::ELEMS);
+        directb_store<T, true, true>(g, acc, cur.bat, cur.m0, cur.tn);
+        if (!more) break;
+        __syncthreads();
+        buf ^= 1;
+        id = nid;
+        cur = nxt;
+    }
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
 }
 
 template <typename T, bool DOT>
@@ -665,6 +845,23 @@ static int launch_directb(GemmArgs& g, bool ta, bool tb, bool nt, hipStream_t st
     const int64_t total = g.tiles_m * g.tiles_n * g.batch;
     if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
     const bool full = g.M % 64 == 0;
+    // Three or more rounds of tiles (four workgroups per CU) with A
+    // transposed and B row-major (the AO->MO transform's two GEMMs): the
+    // persistent kernel. Same box, alternating, bitwise equal: AO->MO half
+    // transform (64 x 786432 x 512) 0.8646 against 0.8787 ms, the transform's
+    // batched GEMM (64 x 320 x 1536 x 512) 0.4702 against 0.4830 ms. At two
+    // rounds (4096^3, 64 x 512^3 without C) it measured 1-2% slower, and its
+    // other layouts spill registers.
+    const int64_t slots = (int64_t)device_cus() / kNumXcd * 4;
+    const bool vecd = ((reinterpret_cast<uintptr_t>(g.D) | (uintptr_t)(g.ldd * sizeof(T)) |
+                        (uintptr_t)(g.sD * sizeof(T))) & 15) == 0;
+    if (!DOT && ta && !tb && full && !g.C && vecd && g.N % BN == 0 && g.K >= kBK && g.K % kBK == 0 &&
+        total >= 3 * slots * kNumXcd) {
+        const dim3 grid((unsigned)(slots * kNumXcd)), block(kThreads);
+        if (nt) hipLaunchKernelGGL((gemm_directb_persistent_kernel<T, true, false, true>), grid, block, 0, st, g);
+        else hipLaunchKernelGGL((gemm_directb_persistent_kernel<T, true, false, false>), grid, block, 0, st, g);
+        return check_launch("tt_gemm");
+    }
     const dim3 grid((unsigned)total), block(kThreads);
 #define TT_DIRECTB_CASE(F, A_T, B_T, N_T)                         \
     if (full == F && ta == A_T && tb == B_T && nt == N_T)         \

@@ -650,8 +650,11 @@ static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
 
 // Device address of `scratch` on the current device, looked up once per
-// device (with that device current) and kept.
-static int mp2_scratch_ptr(void** out) {
+// device (with that device current) and kept. The lookup is a runtime call
+// that may load the code object, which a stream capture must not record: a
+// first call on a device while `st` is capturing is refused (the caller makes
+// one eager call on each device before capturing).
+static int mp2_scratch_ptr(hipStream_t st, void** out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(TT_HIP_ERROR, "tt_mp2_energy_noalloc: hipGetDevice: %s", hipGetErrorString(e));
@@ -659,6 +662,15 @@ static int mp2_scratch_ptr(void** out) {
         return set_error(TT_UNSUPPORTED, "tt_mp2_energy_noalloc: device index %d beyond %d", dev, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess)
+            return set_error(TT_HIP_ERROR, "tt_mp2_energy_noalloc: hipStreamIsCapturing: %s", hipGetErrorString(e));
+        if (cs != hipStreamCaptureStatusNone)
+            return set_error(TT_INVALID,
+                             "tt_mp2_energy_noalloc: first call on device %d made under stream capture; make one "
+                             "call on each device before capturing (it looks up the scratch address)",
+                             dev);
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
@@ -700,7 +712,7 @@ extern "C" int tt_mp2_energy_noalloc(int dtype, int64_t nocc, int64_t nvir, int6
                          "%lld (use tt_mp2_energy with a workspace, or deterministic=0)",
                          (long long)nocc, (long long)nvir, (long long)need, (long long)kMp2ScratchDoubles);
     void* ws = nullptr;
-    rc = mp2_scratch_ptr(&ws);
+    rc = mp2_scratch_ptr(static_cast<hipStream_t>(stream), &ws);
     if (rc != TT_OK) return rc;
     // The scratch holds the partials only: no padded copy of B.
     return mp2_dispatch(dtype, nocc, nvir, naux, B, eps_occ, eps_vir, energy_out, ws, 0, deterministic,

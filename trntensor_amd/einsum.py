@@ -121,12 +121,14 @@ def _run(subscripts, operands, plan, alpha, beta, out, cd_override):
     terms = lhs.split(",")
 
     prefer_gemm = plan.strategy in ("matmul", "bmm")
-    if res_dtype.is_complex or not res_dtype.is_floating_point:
-        # Integer and complex results: the contraction alone on the kernels,
-        # then the reference's two scalar passes (trntensor/einsum.py:99-102)
-        # under torch's promotion rules: an integer result times a float
-        # alpha becomes float32, complex scalars rotate the parts, an integral
-        # result takes only an integral beta.
+    if res_dtype.is_complex or not res_dtype.is_floating_point or isinstance(alpha, complex) or isinstance(beta, complex):
+        # Integer and complex results, and complex scalars: the contraction
+        # alone on the kernels, then the reference's two scalar passes
+        # (trntensor/einsum.py:99-102) under torch's promotion rules: an
+        # integer result times a float alpha becomes float32, a complex alpha
+        # makes a real result complex, complex scalars rotate the parts, an
+        # integral result takes only an integral beta and a real one only a
+        # real beta.
         res = _contract(terms, out_str, ops, plan, 1.0, 0.0, None, prefer_gemm)
         if res.dtype != res_dtype:
             res = res.to(res_dtype)

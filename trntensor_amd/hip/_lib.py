@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 TT_OK, TT_INVALID, TT_UNSUPPORTED, TT_HIP_ERROR = 0, 1, 2, 3
 TT_F32, TT_F64, TT_F64_DD, TT_BF16, TT_F16, TT_I64 = 0, 1, 2, 3, 4, 5
 TT_MAX_DIMS = 8
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every symbol include/trntensor_hip.h declares, with its ctypes signature.
 _i64 = ctypes.c_int64
@@ -49,6 +49,7 @@ SIGNATURES = {
     "tt_ao_to_mo_workspace_bytes": (_sz, [_int, _i64, _i64, _i64, _i64]),
     "tt_ao_to_mo_transform": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tt_mfma_rate_probe": (_int, [_int, _i64, _i64, _vp, _vp]),
+    "tt_hbm_probe": (_int, [_int, _vp, _vp, _i64, _i64, _vp, _vp]),
     "tt_strided_contract_workspace_bytes": (_sz, [_int, _int, _i64p, _int, _i64p]),
     "tt_strided_contract": (
         _int,

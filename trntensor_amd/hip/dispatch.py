@@ -171,6 +171,28 @@ def compute_dtype(dt: torch.dtype) -> torch.dtype:
 # ---------------------------------------------------------------------------
 # entry points replacing the reference's NKI dispatchers
 # ---------------------------------------------------------------------------
+def _mp2_workspace(lib, code: int, nocc: int, nvir: int, naux: int, device: torch.device,
+                   _alloc=None) -> tuple[torch.Tensor, int]:
+    """Workspace for tt_mp2_energy: (tensor, bytes).
+
+    When naux is not a multiple of 16 the full query includes a row-padded
+    copy of B (as many bytes as B itself, rounded up), which makes the call
+    5-7% faster with the same energy bitwise. If the device cannot hold that
+    copy, the call runs on B as given with a workspace of the partials only
+    (the query for naux rounded up to 16). `_alloc` replaces torch.empty in
+    tests.
+    """
+    alloc = _alloc or (lambda n: torch.empty(n, dtype=torch.uint8, device=device))
+    full = int(lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux))
+    part = int(lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, (naux + 15) // 16 * 16))
+    if full > part:
+        try:
+            return alloc(full), full
+        except torch.OutOfMemoryError:
+            pass
+    return alloc(max(part, 1)), part
+
+
 def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
     """Fused DF-MP2 energy on tt_mp2_energy (reference _nki_mp2_energy, dispatch.py:240-283).
 
@@ -191,8 +213,7 @@ def _hip_mp2_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     ev = ev.to(cd).contiguous()
     nocc, nvir, naux = b.shape
     code = engine.dtype_code(cd)
-    wsb = lib.tt_mp2_energy_workspace_bytes(code, nocc, nvir, naux)
-    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=b.device)
+    ws, wsb = _mp2_workspace(lib, code, nocc, nvir, naux, b.device)
     e = torch.empty((), dtype=cd, device=b.device)
     st = lib.tt_mp2_energy(
         code,

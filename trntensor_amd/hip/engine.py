@@ -311,6 +311,7 @@ def gemm(
     sC: int = 0,
     a_off: int = 0,
     b_off: int = 0,
+    d_off: int = 0,
 ) -> None:
     """tt_gemm on torch tensors (pointers taken at the given element offsets)."""
     lib = _lib.load()
@@ -333,7 +334,7 @@ def gemm(
         _ptr(C),
         ldc,
         sC,
-        _ptr(D),
+        D.data_ptr() + d_off * es,
         ldd,
         sD,
         batch,
