@@ -696,6 +696,16 @@ def bench_c1(torch, tt, dev, args):
         return run
 
     t_dev = per_call(synced(dev_loop), 20)
+    # Host cost per call alone: the 64 launches enqueued back to back (the
+    # queue holds them all), timed before the synchronisation.
+    host = []
+    for _ in range(20):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dev_loop()
+        host.append((time.perf_counter() - t0) / 64)
+    torch.cuda.synchronize()
+    res["device_einsum_host_us_per_call"] = round(statistics.median(host) * 1e6, 2)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):

@@ -83,6 +83,18 @@ int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
             void* D, int64_t ldd, int64_t strideD, int64_t batch, void* stream);
 
 /*
+ * tt_gemm with its integer launch parameters in one array, for callers that
+ * launch the same contraction shape many times and keep the array: params =
+ * {dtype, transA, transB, M, N, K, lda, strideA, ldb, strideB, ldc, strideC,
+ * ldd, strideD, batch} (15 values). Same checks, kernels and results as
+ * tt_gemm. No counterpart in the reference: it shortens the host path of a
+ * small device-resident einsum on a plan-cache hit (the Python front-end
+ * passes 8 arguments instead of 22 through its FFI).
+ */
+int tt_gemm_packed(const int64_t* params, double alpha, double beta, const void* A, const void* B,
+                   const void* C, void* D, void* stream);
+
+/*
  * Workspace (device bytes) that tt_gemm_dot needs.
  */
 size_t tt_gemm_dot_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t batch);

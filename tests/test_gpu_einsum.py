@@ -648,3 +648,77 @@ class TestIntegerAndComplex:
             cpu_ref.einsum("ij,jk->ik", A, B, beta=1j, out=outr)
         with pytest.raises(RuntimeError, match="complex"):
             trntensor.einsum("ij,jk->ik", A.cuda(), B.cuda(), beta=1j, out=outr.cuda())
+
+
+class TestLaunchCache:
+    """Repeat calls of a two-operand contraction that runs as one GEMM launch
+    go through a cached launcher (one allocation, one library call). They must
+    be indistinguishable from the first call: same values bitwise, a miss for
+    any other shape, stride, dtype or keyword, planning again after
+    clear_plan_cache, and the backend switch still honoured."""
+
+    def _cache(self):
+        from trntensor_amd import plan
+
+        return plan._LAUNCH_CACHE
+
+    @pytest.mark.parametrize("sub,shapes,dt", [
+        ("ap,bp->ab", [(32, 96), (32, 96)], torch.float32),
+        ("ij,jk->ik", [(70, 50), (50, 130)], torch.float64),
+        ("bij,bjk->bik", [(3, 40, 20), (3, 20, 64)], torch.float32),
+        ("ij,kj->ik", [(64, 48), (80, 48)], torch.bfloat16),
+    ])
+    def test_repeat_calls_bitwise(self, hip, sub, shapes, dt):
+        g = torch.Generator().manual_seed(4)
+        ops = [torch.randn(*s, generator=g).to(dt).cuda() for s in shapes]
+        trntensor.clear_plan_cache()
+        first = trntensor.einsum(sub, *ops)
+        assert len(self._cache()) == 1
+        for alpha in (1.0, 2.5, 3):
+            again = trntensor.einsum(sub, *ops, alpha=alpha)
+            ref = trntensor.einsum(sub, *ops, alpha=alpha, beta=0.0, out=torch.zeros_like(first))  # planned path
+            assert again.dtype == first.dtype and again.shape == first.shape and again.device == first.device
+            assert torch.equal(again, ref)
+        assert torch.equal(trntensor.einsum(sub, *ops), first)
+        want = cpu_ref.einsum(sub, *[o.cpu().double() for o in ops])
+        assert normwise(first.cpu().double(), want) <= (1e-2 if dt == torch.bfloat16 else {torch.float32: 1e-5, torch.float64: 1e-12}[dt])
+
+    def test_misses_and_clear(self, hip):
+        g = torch.Generator().manual_seed(5)
+        B = torch.randn(8, 32, 96, generator=g).cuda()
+        trntensor.clear_plan_cache()
+        trntensor.einsum("ap,bp->ab", B[0], B[1])
+        trntensor.einsum("ap,bp->ab", B[2], B[3])  # same shapes and strides: a hit
+        assert len(self._cache()) == 1
+        Bt = B.transpose(1, 2).contiguous().transpose(1, 2)  # same shape, other strides
+        got = trntensor.einsum("ap,bp->ab", Bt[0], Bt[1])
+        assert torch.equal(got, trntensor.einsum("ap,bp->ab", B[0], B[1]))
+        assert len(self._cache()) == 2
+        trntensor.einsum("ap,bp->ab", B[0].double(), B[1].double())
+        assert len(self._cache()) == 3
+        trntensor.clear_plan_cache()
+        assert len(self._cache()) == 0 and trntensor.plan_cache_info()["size"] == 0
+        trntensor.einsum("ap,bp->ab", B[0], B[1])
+        assert trntensor.plan_cache_info()["size"] == 1
+
+    def test_backend_switch_applies_to_cached_launches(self, hip):
+        B = torch.randn(4, 32, 96).cuda()
+        trntensor.einsum("ap,bp->ab", B[0], B[1])
+        trntensor.einsum("ap,bp->ab", B[0], B[1])
+        try:
+            trntensor.set_backend("pytorch")
+            with pytest.raises(RuntimeError, match="pytorch"):
+                trntensor.einsum("ap,bp->ab", B[0], B[1])
+        finally:
+            trntensor.set_backend("auto")
+
+    def test_keywords_bypass_the_cache(self, hip):
+        g = torch.Generator().manual_seed(6)
+        A, Bm, C = (torch.randn(40, 40, generator=g).cuda() for _ in range(3))
+        plain = trntensor.einsum("ij,jk->ik", A, Bm)
+        withc = trntensor.einsum("ij,jk->ik", A, Bm, alpha=2.0, beta=0.5, out=C)
+        ref = cpu_ref.einsum("ij,jk->ik", A.cpu(), Bm.cpu(), alpha=2.0, beta=0.5, out=C.cpu())
+        assert normwise(withc.cpu(), ref) <= 1e-5
+        assert normwise(plain.cpu(), cpu_ref.einsum("ij,jk->ik", A.cpu(), Bm.cpu())) <= 1e-5
+        kah = trntensor.einsum("ij,jk->ik", A, Bm, precision="kahan")
+        assert normwise(kah.cpu(), cpu_ref.einsum("ij,jk->ik", A.cpu(), Bm.cpu(), precision="kahan")) <= 2e-7

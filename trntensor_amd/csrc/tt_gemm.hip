@@ -1049,6 +1049,14 @@ extern "C" int tt_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, 
     return gemm_dispatch(dtype, transA != 0, transB != 0, g, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int tt_gemm_packed(const int64_t* params, double alpha, double beta, const void* A, const void* B,
+                              const void* C, void* D, void* stream) {
+    if (!params) return tt::set_error(TT_INVALID, "tt_gemm_packed: params is NULL");
+    const int64_t* p = params;
+    return tt_gemm((int)p[0], (int)p[1], (int)p[2], p[3], p[4], p[5], alpha, A, p[6], p[7], B, p[8], p[9], beta, C,
+                   p[10], p[11], D, p[12], p[13], p[14], stream);
+}
+
 extern "C" size_t tt_gemm_dot_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t batch) {
     (void)dtype;
     if (M <= 0 || N <= 0 || batch <= 0) return 256;

@@ -13,7 +13,7 @@ import torch
 
 from .hip import dispatch
 from .hip import engine
-from .plan import ContractionPlan, _parse_subscripts, plan_contraction
+from .plan import _LAUNCH_CACHE, _LAUNCH_CACHE_MAX, _PLAN_CACHE, ContractionPlan, _parse_subscripts, _shape_key, plan_contraction
 
 _DTYPE_MAP: dict[str, torch.dtype] = {
     "bf16": torch.bfloat16,
@@ -69,11 +69,46 @@ def einsum(
         einsum("mi,mnP->inP", C_occ, eri)        # AO->MO half transform
         einsum("ia,jb,abP,ijP->", A, B, W, V)    # greedy path
     """
+    # Repeat call of a two-operand contraction that runs as one GEMM launch:
+    # the launcher cached on its first call (plan cached, same shapes,
+    # strides, dtypes and devices), one allocation and one library call.
+    plain = (len(operands) == 2 and out is None and dtype is None and precision == "fast" and optimize == "greedy"
+             and type(alpha) in (float, int))
+    if plain:
+        a, b = operands
+        key = (subscripts, a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, b.device)
+        run = _LAUNCH_CACHE.get(key)
+        if run is not None and dispatch._use_hip():
+            res = run(a, b, float(alpha))
+            if res is not None:
+                return res
     target = _resolve_dtype(dtype)
     if target is not None:
         operands = tuple(op.to(target) for op in operands)
     plan = plan_contraction(subscripts, *operands, precision=precision, optimize=optimize)
-    return _execute_contraction(subscripts, operands, plan, alpha=alpha, beta=beta, out=out)
+    res = _execute_contraction(subscripts, operands, plan, alpha=alpha, beta=beta, out=out)
+    if plain:
+        _remember_launch(key, subscripts, plan, a, b)
+    return res
+
+
+_FAST_DTYPES = (torch.float32, torch.float64, torch.bfloat16, torch.float16)
+
+
+def _remember_launch(key, subscripts, plan, a, b) -> None:
+    """Cache the launcher of a just-run two-operand contraction when both
+    operands are on one HIP device in one real dtype and the engine ran it
+    as one in-place GEMM launch (its recipe is cached)."""
+    if (plan.strategy == "path" or a.device.type != "cuda" or b.device != a.device or a.dtype != b.dtype
+            or a.dtype not in _FAST_DTYPES or _PLAN_CACHE.get(_shape_key(subscripts, (a, b))) is not plan):
+        return
+    lhs, out_str = _parse_subscripts(subscripts)
+    ta, tb = lhs.split(",")
+    run = engine.fast_launcher(ta, tb, out_str, a, b, plan.strategy in ("matmul", "bmm"))
+    if run is not None:
+        if len(_LAUNCH_CACHE) >= _LAUNCH_CACHE_MAX:
+            _LAUNCH_CACHE.clear()
+        _LAUNCH_CACHE[key] = run
 
 
 def _execute_contraction(

@@ -35,6 +35,7 @@ SIGNATURES = {
         _int,
         [_int, _int, _int, _i64, _i64, _i64, _dbl, _vp, _i64, _i64, _vp, _i64, _i64, _dbl, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp],
     ),
+    "tt_gemm_packed": (_int, [_vp, _dbl, _dbl, _vp, _vp, _vp, _vp, _vp]),
     "tt_gemm_dot_workspace_bytes": (_sz, [_int, _i64, _i64, _i64]),
     "tt_gemm_dot": (
         _int,
@@ -77,7 +78,7 @@ def load():
             fn.argtypes = args
         if lib.tt_abi_version() != ABI_VERSION:
             raise OSError(f"ABI version {lib.tt_abi_version()} != {ABI_VERSION}")
-    except OSError as exc:
+    except (OSError, AttributeError) as exc:  # AttributeError: a symbol the header declares is missing
         _load_error = f"cannot load {LIB_PATH}: {exc}"
         return None
     _lib = lib

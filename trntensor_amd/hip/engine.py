@@ -455,9 +455,50 @@ class _GemmRecipe:
         return D
 
 
+    def launcher(self, device: torch.device):
+        """A callable (A, B, alpha) -> D that repeats this recipe's one
+        tt_gemm launch (no C) through tt_gemm_packed, with the integer launch
+        parameters kept in one array; None if the recipe needs more than one
+        launch (K split). For callers that have checked the operands against
+        the recipe's key (shapes, strides, dtype, device)."""
+        if self.split > 1 or self.dt not in (torch.float32, torch.float64, torch.bfloat16, torch.float16):
+            return None
+        lib = _lib.load()
+        fn = lib.tt_gemm_packed
+        code = dtype_code(self.dt)
+        params = (ctypes.c_int64 * 15)(code, int(self.ta), int(self.tb), self.M, self.N, self.K, self.lda, self.sA,
+                                       self.ldb, self.sB, 0, 0, self.ldd, self.sD, self.batch)
+        pp = ctypes.addressof(params)
+        shape, dt, swap = self.shape, self.dt, self.swap
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        empty, raw, acc = torch.empty, _raw_stream, _ACCUMULATION
+        if raw is None:
+            return None
+
+        def run(a, b, alpha):
+            if acc.get() != "native":
+                return None
+            D = empty(shape, dtype=dt, device=device)
+            x, y = (b, a) if swap else (a, b)
+            st = fn(pp, alpha, 0.0, x.data_ptr(), y.data_ptr(), None, D.data_ptr(), raw(idx))
+            if st:
+                _lib.check(st, "tt_gemm")
+            return D
+
+        run.params = params  # keeps the array alive with the callable
+        return run
+
+
 # Recipes keyed by (terms, out, shapes, strides, dtype, prefer_gemm); bounded.
 _RECIPES: dict[tuple, _GemmRecipe] = {}
 _RECIPES_MAX = 4096
+
+
+def fast_launcher(ta: str, tb: str, out: str, a: torch.Tensor, b: torch.Tensor, prefer_gemm: bool):
+    """The launcher of the cached recipe for this two-operand contraction
+    (see _GemmRecipe.launcher), or None when there is none."""
+    rec = _RECIPES.get((ta, tb, out, a.shape, a.stride(), b.shape, b.stride(), a.dtype, prefer_gemm))
+    return None if rec is None else rec.launcher(a.device)
 
 
 def _gemm_layout(op: Operand, rows: list[str], ks: list[str]):

@@ -95,6 +95,12 @@ def _validate_subscripts(subscripts: str, operands: tuple) -> None:
 
 
 _PLAN_CACHE: dict[tuple, ContractionPlan] = {}
+# Launchers of two-operand contractions whose plan is cached and which run as
+# one GEMM launch, keyed by subscripts and both operands' shapes, strides,
+# dtypes and devices (filled and read by the einsum front-end; emptied with
+# the plan cache, so a call after clear_plan_cache plans again).
+_LAUNCH_CACHE: dict[tuple, object] = {}
+_LAUNCH_CACHE_MAX = 4096
 
 # Path searches for 3+ operands. "greedy" is the reference's rule and the
 # default; "optimal" is opt-in (no counterpart in the reference).
@@ -115,6 +121,7 @@ def _shape_key(subscripts: str, operands: tuple, precision: str = "fast", optimi
 def clear_plan_cache() -> None:
     """Discard all cached contraction plans."""
     _PLAN_CACHE.clear()
+    _LAUNCH_CACHE.clear()
 
 
 def plan_cache_info() -> dict[str, int]:
