@@ -436,3 +436,36 @@ def test_gemm_persistent_matches_per_tile_kernel(hip, dt, M, ntiles, K, batch, a
     ref = alpha * torch.bmm(A[:, :, :].transpose(1, 2).double().cpu(), B[:, :, cols].double().cpu())
     assert normwise(D[:, :, cols].cpu(), ref) <= TOL[dt]
     assert not torch.isnan(D).any()
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("M,N,K,batch", [(32, 32, 96, 1), (32, 32, 128, 3), (17, 29, 64, 2), (1, 32, 5, 1),
+                                         (32, 7, 33, 5), (32, 32, 64, 1), (30, 31, 127, 1)])
+@pytest.mark.parametrize("alpha,beta,with_c", [(1.0, 0.0, False), (1.5, 0.5, True)])
+def test_gemm_small_tile_matches_wide_tiles(hip, dt, M, N, K, batch, alpha, beta, with_c):
+    """M, N <= 32 with both operands k-contiguous and K within one deep stage
+    (config 1's 'ap,bp->ab', 32 x 32 x 96): the 32 x 32 single-stage tile.
+    Checked against float64 torch, and bitwise against the same outputs as
+    part of a wider problem (M = 40 takes the 64-row tiles; the extra rows
+    do not change the first M), which keeps the k order per output."""
+    from trntensor_amd.hip import engine
+
+    g = torch.Generator().manual_seed(M * 7 + N + K + batch)
+    dev = torch.device("cuda")
+    Mw = 40
+    A = torch.randn(batch, Mw, K, generator=g, dtype=torch.float64)
+    B = torch.randn(batch, N, K, generator=g, dtype=torch.float64)
+    C = torch.randn(batch, Mw, N, generator=g, dtype=torch.float64)
+    ref = alpha * torch.bmm(A[:, :M], B.transpose(1, 2).contiguous())
+    if with_c:
+        ref = ref + beta * C[:, :M]
+    Ad, Bd, Cd = A.to(dev, dt), B.to(dev, dt), C.to(dev, dt)
+    outs = []
+    for m in (M, Mw):
+        D = torch.full((batch, Mw, N), float("nan"), dtype=dt, device=dev)
+        engine.gemm(False, True, m, N, K, Ad, K, Mw * K, Bd, K, N * K, D, N, Mw * N, batch, alpha, beta,
+                    Cd if with_c else None, N, Mw * N)
+        outs.append(D[:, :M])
+    torch.cuda.synchronize()
+    assert normwise(outs[0], ref) <= TOL[dt]
+    assert torch.equal(outs[0], outs[1])

@@ -575,13 +575,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         };
         aload(0);
         sa.store(lds);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            if (nfull > 0) bload(0, p);
-            else bload_tail(0, p);
-        }
-        __syncthreads();
         int64_t t = 0;
+        // Only the vector loads of B lead into the main loop: with the
+        // element-wise tail loads joining them there, the compiler's wait at
+        // the top of each stage covered every outstanding load (same box,
+        // alternating, bitwise equal: 4096^3 fp32 1.0135 against 1.0172 ms,
+        // 64 x 512^3 with alpha/beta 0.1441 against 0.1456 ms fp32 and 0.2639
+        // against 0.2669 ms fp64).
+        if (nfull == 0) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) bload_tail(0, p);
+            __syncthreads();
+        } else {  // the main loop below is this branch's (closed after it)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) bload(0, p);
+            __syncthreads();
         for (; t + 1 < nfull; ++t) {
             // Stage t + 1 of A goes to the other buffer; B piece p is reloaded
             // for stage t + 1 as soon as its MFMAs have issued. With B
@@ -600,10 +608,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 bload(t + 1, p);
             }
             if (sizeof(T) == 8 && TB) __builtin_amdgcn_s_setprio(0);
+            if constexpr (sizeof(T) == 4 && !TB) {
+                // A's loads, then each piece's MFMAs followed by its
+                // next-stage B load; left to itself the compiler issued the
+                // four B loads together near the end of the stage (same box,
+                // alternating, bitwise equal: 4096^3 1.0036 against 1.0135
+                // ms, 64 x 512^3 with alpha/beta 0.1437 against 0.1441 ms; in
+                // fp64 4096^3 measured 1% slower with it).
+                __builtin_amdgcn_sched_group_barrier(0x020, SA::NC, 0);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NB, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
             sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
             __syncthreads();
         }
+        }  // nfull > 0
         if (t + 1 < nk) {
             // The partial last stage (K not a multiple of 16).
             aload(t + 1);
@@ -899,6 +922,23 @@ static int launch_tile(GemmArgs& g, bool ta, bool tb, bool vec, hipStream_t st) 
     return check_launch("tt_gemm");
 }
 
+// Small problems: 32 x 32 tiles (four 16 x 16 wave tiles) and one stage that
+// holds all of K, so a launch makes one round trip to memory instead of one
+// per 16-deep stage. Both operands k-contiguous (A not transposed, B
+// transposed), the layouts whose 32-row stage the staging supports. The k
+// order per output is the other tiles' (16-deep passes in order).
+template <typename T, int BK>
+static int launch_small(GemmArgs& g, bool vec, hipStream_t st) {
+    g.tiles_m = (g.M + 31) / 32;
+    g.tiles_n = (g.N + 31) / 32;
+    const int64_t total = g.tiles_m * g.tiles_n * g.batch;
+    if (total > 0x7fffffffLL) return set_error(TT_UNSUPPORTED, "tt_gemm: %lld tiles exceed one launch", (long long)total);
+    const dim3 grid((unsigned)total), block(kThreads);
+    if (vec) hipLaunchKernelGGL((gemm_kernel<T, 32, 32, 1, 1, false, true, true, false, 1, BK, false>), grid, block, 0, st, g);
+    else hipLaunchKernelGGL((gemm_kernel<T, 32, 32, 1, 1, false, true, false, false, 1, BK, false>), grid, block, 0, st, g);
+    return check_launch("tt_gemm");
+}
+
 template <typename T, bool DOT>
 static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     constexpr int V = Vec16<T>::n;
@@ -906,6 +946,13 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 16-byte vectors need aligned bases, leading dimensions and batch strides.
     bool vec = ok16(g.A) && ok16(g.B) && g.lda % V == 0 && g.ldb % V == 0;
     if (g.batch > 1) vec = vec && g.sA % V == 0 && g.sB % V == 0;
+    // One 32 x 32 tile per batch entry and K within one deep stage (the
+    // DF-MP2 pair block 'ap,bp->ab' of config 1: 32 x 32 x 96).
+    constexpr int64_t KS = 512 / sizeof(T);  // 128 fp32, 64 fp64
+    if (!DOT && !ta && tb && g.M <= 32 && g.N <= 32 && g.K <= KS) {
+        if (g.K <= KS / 2) return launch_small<T, KS / 2>(g, vec, st);
+        return launch_small<T, KS>(g, vec, st);
+    }
     // Small-M (e.g. the AO->MO half transform, M = nocc): 64 x 128 tiles of
     // four 32 x 64 wavefront tiles keep registers and LDS low enough for
     // several workgroups per CU, i.e. more loads in flight on a long stream.
