@@ -317,7 +317,20 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
     const int64_t u = task - pair * g.npq;
     int i, j, p, q;
     tri_decode(pair, g.nocc, i, j);
-    tri_decode(u, g.nblk, p, q);
+    // Within a pair the nblk (nblk - 1) / 2 off-diagonal units come first
+    // (row-major over p < q), then the nblk diagonal ones. A diagonal unit
+    // issues half the MFMAs per stage and runs ahead of the off-diagonal
+    // units reading the same panels; grouped, each kind stays closer to its
+    // own pace. Same box, alternating: config 4 fp64 7.599 against 7.624 ms
+    // and 7.649 against 7.669 ms, fp32 3.946 against 3.956 ms, naux 2400
+    // 15.59 against 15.64 ms.
+    const int64_t noff = (int64_t)g.nblk * (g.nblk - 1) / 2;
+    if (u < noff) {
+        tri_decode(u, g.nblk - 1, p, q);
+        q += 1;
+    } else {
+        p = q = (int)(u - noff);
+    }
     // Y source: 0 = MFMA (i < j, p < q), 1 = X itself (i = j, p < q), 2 = X^T (p = q).
     const int ymode = (p == q) ? 2 : (i == j ? 1 : 0);
 
