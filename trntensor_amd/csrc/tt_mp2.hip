@@ -31,6 +31,13 @@ namespace tt {
 
 constexpr int kMp2Threads = 256;
 constexpr int kMp2Tile = 64;
+// Occupied pairs per group of the unit order (see mp2_energy_kernel). Same
+// box, one process, alternating, against one pair per group: config 4 fp64
+// 7.366 against 7.477 ms and 7.393 against 7.500 ms, fp32 3.932 against
+// 3.961 ms, naux 2400 fp64 15.33 against 15.42 ms, nocc 128 / nvir 640 /
+// naux 2400 243.0 against 243.2 ms (groups of 8: 7.401, 3.960, 15.26, 241.8;
+// of 64: 7.389, 3.902, 15.31, 243.4).
+constexpr int kMp2PairGroup = 16;
 #ifndef TT_MP2_STAGE_K
 #define TT_MP2_STAGE_K 16
 #endif
@@ -313,18 +320,32 @@ __global__ __launch_bounds__(kMp2Threads) void mp2_energy_kernel(Mp2Args g) {
 
     const int64_t local = xcd_remap(blockIdx.x, g.ntasks);
     const int64_t task = g.first + local;
-    const int64_t pair = task / g.npq;
-    const int64_t u = task - pair * g.npq;
+    // Unit order: groups of kMp2PairGroup occupied pairs; within a group, the
+    // off-diagonal units (p < q) of all its pairs first, pair-major and
+    // row-major over p < q, then its diagonal units (p = q). A diagonal unit
+    // issues half the MFMAs per stage and runs ahead of the off-diagonal
+    // units that read the same panels; grouped, each kind keeps the pace of
+    // the units it shares panels with, and short units end each group.
+    const int64_t noff = (int64_t)g.nblk * (g.nblk - 1) / 2;  // off-diagonal units per pair
+    int64_t pair, u;
+    {
+        const int64_t npairs = (int64_t)g.nocc * (g.nocc + 1) / 2;
+        const int64_t grp = task / (kMp2PairGroup * g.npq);
+        const int64_t gp = min((int64_t)kMp2PairGroup, npairs - grp * kMp2PairGroup);  // pairs in this group
+        const int64_t r = task - grp * kMp2PairGroup * g.npq;
+        if (r < gp * noff) {
+            pair = grp * kMp2PairGroup + r / noff;
+            u = r % noff;
+        } else {
+            const int64_t r2 = r - gp * noff;
+            pair = grp * kMp2PairGroup + r2 / g.nblk;
+            u = noff + r2 % g.nblk;
+        }
+    }
     int i, j, p, q;
     tri_decode(pair, g.nocc, i, j);
-    // Within a pair the nblk (nblk - 1) / 2 off-diagonal units come first
-    // (row-major over p < q), then the nblk diagonal ones. A diagonal unit
-    // issues half the MFMAs per stage and runs ahead of the off-diagonal
-    // units reading the same panels; grouped, each kind stays closer to its
-    // own pace. Same box, alternating: config 4 fp64 7.599 against 7.624 ms
-    // and 7.649 against 7.669 ms, fp32 3.946 against 3.956 ms, naux 2400
-    // 15.59 against 15.64 ms.
-    const int64_t noff = (int64_t)g.nblk * (g.nblk - 1) / 2;
+    // u < noff: the off-diagonal units in row-major order over p < q; then
+    // the diagonal ones.
     if (u < noff) {
         tri_decode(u, g.nblk - 1, p, q);
         q += 1;
