@@ -124,6 +124,9 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
         (True, 320, 1536, 512, 2, 1.0, 0.0, False, 0),  # the AO->MO transform's second GEMM
         (False, 200, 256, 333, 3, -1.0, 1.0, True, 1),  # ragged M and K
         (True, 70, 384, 1000, 2, 2.0, 0.0, False, 0),
+        # more than 64 row tiles: rows in groups of 16 slabs sweeping every column tile
+        (False, 4160, 512, 48, 1, 1.5, 0.5, True, 0),
+        (True, 4200, 768, 40, 2, 1.0, 0.0, False, 1),  # ragged last group and rows
     ],
 )
 def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
@@ -223,6 +226,7 @@ def test_gemm_direct_b_k_contiguous_matches_lds_tile(hip, ta, M, N, K, batch, al
         (False, True, 64, 256, 100, 2, False),  # M = 64: non-temporal B loads
         (True, False, 128, 384, 37, 3, True),  # K tail, B row-major
         (True, True, 192, 128, 16, 1, False),
+        (False, True, 4224, 256, 64, 1, True),  # 66 row tiles: the grouped row order of config 5's GEMM
     ],
 )
 def test_gemm_dot_direct_b_matches_lds_tile(hip, ta, tb, M, N, K, batch, with_e2):
