@@ -205,3 +205,21 @@ def test_mp2_shard_range_checks_need_no_device(lib):
     assert st == _lib.TT_INVALID and b"outside" in lib.tt_last_error()  # 10 pairs x 3 block pairs = 30 units
     st = lib.tt_mp2_energy_shard(1, 4, 70, 16, dummy, dummy, dummy, -1, 2, dummy, dummy, ws, 1, None)
     assert st == _lib.TT_INVALID
+
+
+def test_launch_table_loads_and_misses_without_a_device(lib):
+    """The host launch table (tt_fastpath.so) loads against the library's
+    entry points; a lookup of CPU operands is a miss (no launch), and only
+    operands on one GPU in one dtype can be recorded."""
+    from trntensor_amd.hip import _fastpath
+
+    assert os.path.exists(_fastpath.PATH), "tt_fastpath.so is not built"
+    tab = _fastpath.table(8)
+    assert tab is not None, _fastpath.error()
+    a, b = torch.randn(32, 96), torch.randn(32, 96)
+    assert tab.run("ap,bp->ab", a, b, 1.0) is None
+    with pytest.raises(RuntimeError, match="one device"):
+        tab.add("ap,bp->ab", a, b, [0] * 15, [32, 32], False)
+    with pytest.raises(TypeError):
+        tab.run("ap,bp->ab", a.numpy(), b, 1.0)
+    assert len(tab) == 0

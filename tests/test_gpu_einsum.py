@@ -7,6 +7,8 @@ restated) as the expected value and normwise bars of 1e-12 (float64) /
 1e-5 (float32). The config classes run BASELINE.json's shapes.
 """
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -657,10 +659,8 @@ class TestLaunchCache:
     any other shape, stride, dtype or keyword, planning again after
     clear_plan_cache, and the backend switch still honoured."""
 
-    def _cache(self):
-        from trntensor_amd import plan
-
-        return plan._LAUNCH_CACHE
+    def _size(self):
+        return importlib.import_module("trntensor_amd.einsum")._launch_cache_size()
 
     @pytest.mark.parametrize("sub,shapes,dt", [
         ("ap,bp->ab", [(32, 96), (32, 96)], torch.float32),
@@ -673,7 +673,7 @@ class TestLaunchCache:
         ops = [torch.randn(*s, generator=g).to(dt).cuda() for s in shapes]
         trntensor.clear_plan_cache()
         first = trntensor.einsum(sub, *ops)
-        assert len(self._cache()) == 1
+        assert self._size() == 1
         for alpha in (1.0, 2.5, 3):
             again = trntensor.einsum(sub, *ops, alpha=alpha)
             ref = trntensor.einsum(sub, *ops, alpha=alpha, beta=0.0, out=torch.zeros_like(first))  # planned path
@@ -689,17 +689,35 @@ class TestLaunchCache:
         trntensor.clear_plan_cache()
         trntensor.einsum("ap,bp->ab", B[0], B[1])
         trntensor.einsum("ap,bp->ab", B[2], B[3])  # same shapes and strides: a hit
-        assert len(self._cache()) == 1
+        assert self._size() == 1
         Bt = B.transpose(1, 2).contiguous().transpose(1, 2)  # same shape, other strides
         got = trntensor.einsum("ap,bp->ab", Bt[0], Bt[1])
         assert torch.equal(got, trntensor.einsum("ap,bp->ab", B[0], B[1]))
-        assert len(self._cache()) == 2
+        assert self._size() == 2
         trntensor.einsum("ap,bp->ab", B[0].double(), B[1].double())
-        assert len(self._cache()) == 3
+        assert self._size() == 3
         trntensor.clear_plan_cache()
-        assert len(self._cache()) == 0 and trntensor.plan_cache_info()["size"] == 0
+        assert self._size() == 0 and trntensor.plan_cache_info()["size"] == 0
         trntensor.einsum("ap,bp->ab", B[0], B[1])
         assert trntensor.plan_cache_info()["size"] == 1
+
+    def test_repeat_calls_use_the_native_launch_table(self, hip):
+        """On the GPU the recorded launches live in the C++ table
+        (tt_fastpath.so), not in Python launchers."""
+        from trntensor_amd import plan
+        from trntensor_amd.hip import _fastpath
+
+        E = importlib.import_module("trntensor_amd.einsum")
+        B = torch.randn(4, 32, 96).cuda()
+        trntensor.clear_plan_cache()
+        first = trntensor.einsum("ap,bp->ab", B[0], B[1])
+        assert E._fast is not None, _fastpath.error()
+        assert type(E._fast).__name__ == "LaunchTable" and len(E._fast) == 1 and len(plan._LAUNCH_CACHE) == 0
+        assert torch.equal(trntensor.einsum("ap,bp->ab", B[0], B[1]), first)
+        planned = trntensor.einsum("ap,bp->ab", B[2], B[3], beta=0.0, out=torch.zeros(32, 32).cuda())
+        assert torch.equal(trntensor.einsum("ap,bp->ab", B[2], B[3]), planned)
+        trntensor.clear_plan_cache()
+        assert len(E._fast) == 0
 
     def test_backend_switch_applies_to_cached_launches(self, hip):
         B = torch.randn(4, 32, 96).cuda()

@@ -1,11 +1,12 @@
 """Build libtrntensor_hip.so for gfx950 from the HIP sources in this directory.
 
-Usage: python trntensor_amd/csrc/build.py [--jobs N]
+Usage: python trntensor_amd/csrc/build.py [--jobs N] [--no-fastpath]
 
 Each source is compiled to an object with hipcc in parallel, then linked
 into ``trntensor_amd/_lib/libtrntensor_hip.so`` (in-tree, so it travels
 with the source tree). Packed-FP32 instruction selection is disabled for all
-device code.
+device code. Then the host launch table (tt_fastpath.cpp, a torch C++
+extension) is built into ``trntensor_amd/_lib/fastpath/``.
 """
 
 from __future__ import annotations
@@ -95,9 +96,40 @@ def build(jobs: int = 4, verbose: bool = False, extra: list[str] | None = None) 
     return LIB
 
 
+FASTPATH_DIR = os.path.join(OUT_DIR, "fastpath")
+FASTPATH = os.path.join(FASTPATH_DIR, "tt_fastpath.so")
+
+
+def build_fastpath(verbose: bool = False) -> str:
+    """Compile tt_fastpath.cpp (host C++ against torch's headers, no device
+    code) into ``_lib/fastpath/tt_fastpath.so``, from scratch each time."""
+    import torch.utils.cpp_extension as ce
+
+    os.makedirs(FASTPATH_DIR, exist_ok=True)
+    for f in os.listdir(FASTPATH_DIR):
+        if f.endswith((".so", ".o")) or f in ("build.ninja", ".ninja_deps", ".ninja_log"):
+            os.remove(os.path.join(FASTPATH_DIR, f))
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    ce.load(
+        "tt_fastpath",
+        [os.path.join(HERE, "tt_fastpath.cpp")],
+        build_directory=FASTPATH_DIR,
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include", f"-I{os.path.join(os.path.dirname(PKG), 'include')}"],
+        extra_ldflags=["-lc10_hip"],
+        with_cuda=False,
+        verbose=verbose,
+    )
+    if not os.path.exists(FASTPATH):
+        raise RuntimeError(f"tt_fastpath build produced no {FASTPATH}")
+    return FASTPATH
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--no-fastpath", action="store_true", help="skip the host C++ launch table")
     args, rest = ap.parse_known_args()
     print(build(args.jobs, args.verbose, rest))
+    if not args.no_fastpath:
+        print(build_fastpath(args.verbose))

@@ -11,9 +11,11 @@ from __future__ import annotations
 
 import torch
 
+from .hip import _fastpath
 from .hip import dispatch
 from .hip import engine
-from .plan import _LAUNCH_CACHE, _LAUNCH_CACHE_MAX, _PLAN_CACHE, ContractionPlan, _parse_subscripts, _shape_key, plan_contraction
+from .plan import (_CLEAR_HOOKS, _LAUNCH_CACHE, _LAUNCH_CACHE_MAX, _PLAN_CACHE, ContractionPlan, _parse_subscripts,
+                   _shape_key, plan_contraction)
 
 _DTYPE_MAP: dict[str, torch.dtype] = {
     "bf16": torch.bfloat16,
@@ -70,45 +72,88 @@ def einsum(
         einsum("ia,jb,abP,ijP->", A, B, W, V)    # greedy path
     """
     # Repeat call of a two-operand contraction that runs as one GEMM launch:
-    # the launcher cached on its first call (plan cached, same shapes,
-    # strides, dtypes and devices), one allocation and one library call.
+    # the launch recorded on its first call (plan cached, same shapes,
+    # strides, dtypes and devices), one allocation and one library call, in
+    # the C++ launch table when it is built, else through a cached ctypes
+    # launcher.
     plain = (len(operands) == 2 and out is None and dtype is None and precision == "fast" and optimize == "greedy"
              and type(alpha) in (float, int))
     if plain:
         a, b = operands
-        key = (subscripts, a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, b.device)
-        run = _LAUNCH_CACHE.get(key)
-        if run is not None and dispatch._use_hip():
-            res = run(a, b, float(alpha))
-            if res is not None:
-                return res
+        fast = _fast
+        if fast is not None:
+            if dispatch._use_hip() and engine._ACCUMULATION.get() == "native":
+                try:
+                    res = fast.run(subscripts, a, b, float(alpha))
+                except TypeError:  # not tensors: planning reports it
+                    res = None
+                if res is not None:
+                    return res
+        else:
+            run = _LAUNCH_CACHE.get(_launch_key(subscripts, a, b))
+            if run is not None and dispatch._use_hip():
+                res = run(a, b, float(alpha))
+                if res is not None:
+                    return res
     target = _resolve_dtype(dtype)
     if target is not None:
         operands = tuple(op.to(target) for op in operands)
     plan = plan_contraction(subscripts, *operands, precision=precision, optimize=optimize)
     res = _execute_contraction(subscripts, operands, plan, alpha=alpha, beta=beta, out=out)
     if plain:
-        _remember_launch(key, subscripts, plan, a, b)
+        _remember_launch(subscripts, plan, a, b)
     return res
 
 
 _FAST_DTYPES = (torch.float32, torch.float64, torch.bfloat16, torch.float16)
 
+# The C++ launch table (hip/_fastpath.py) once the first launch has been
+# recorded, if it is built; None while launches go through _LAUNCH_CACHE.
+_fast = None
 
-def _remember_launch(key, subscripts, plan, a, b) -> None:
-    """Cache the launcher of a just-run two-operand contraction when both
+
+def _launch_key(subscripts, a, b) -> tuple:
+    return (subscripts, a.shape, a.stride(), b.shape, b.stride(), a.dtype, b.dtype, a.device, b.device)
+
+
+def _launch_cache_size() -> int:
+    """Recorded launches (the C++ table's, or the ctypes launchers')."""
+    return len(_fast) if _fast is not None else len(_LAUNCH_CACHE)
+
+
+def _clear_launches() -> None:
+    if _fast is not None:
+        _fast.clear()
+
+
+def _remember_launch(subscripts, plan, a, b) -> None:
+    """Record the launch of a just-run two-operand contraction when both
     operands are on one HIP device in one real dtype and the engine ran it
     as one in-place GEMM launch (its recipe is cached)."""
+    global _fast
     if (plan.strategy == "path" or a.device.type != "cuda" or b.device != a.device or a.dtype != b.dtype
             or a.dtype not in _FAST_DTYPES or _PLAN_CACHE.get(_shape_key(subscripts, (a, b))) is not plan):
         return
     lhs, out_str = _parse_subscripts(subscripts)
     ta, tb = lhs.split(",")
-    run = engine.fast_launcher(ta, tb, out_str, a, b, plan.strategy in ("matmul", "bmm"))
+    rec = engine.cached_recipe(ta, tb, out_str, a, b, plan.strategy in ("matmul", "bmm"))
+    if rec is None:
+        return
+    if _fast is None:
+        _fast = _fastpath.table(_LAUNCH_CACHE_MAX)
+        if _fast is not None:
+            _LAUNCH_CACHE.clear()
+            _CLEAR_HOOKS.append(_clear_launches)
+    if _fast is not None:
+        params = rec.packed_params()
+        if params is not None:
+            _fast.add(subscripts, a, b, params, list(rec.shape), bool(rec.swap))
+        return
+    run = rec.launcher(a.device)
     if run is not None:
         if len(_LAUNCH_CACHE) >= _LAUNCH_CACHE_MAX:
             _LAUNCH_CACHE.clear()
-        _LAUNCH_CACHE[key] = run
+        _LAUNCH_CACHE[_launch_key(subscripts, a, b)] = run
 
 
 def _execute_contraction(

@@ -77,9 +77,30 @@ def get_backend() -> str:
     return _backend
 
 
+# TRNTENSOR_FORCE_BACKEND is read on every call, as the reference does. On
+# CPython, os.environ keeps its encoded entries in a dict (`_data`), which
+# the lookup below reads directly: the same value os.environ.get returns, at
+# a tenth of the cost (0.08 against 0.65 us), which counts on the per-call
+# path of small contractions.
+_FORCE_VAR = "TRNTENSOR_FORCE_BACKEND"
+_ENV_DATA = getattr(os.environ, "_data", None)
+try:
+    _FORCE_KEY = os.environ.encodekey(_FORCE_VAR)  # type: ignore[attr-defined]
+    _decode = os.environ.decodevalue  # type: ignore[attr-defined]
+except AttributeError:
+    _ENV_DATA = None
+
+
+def _forced_backend() -> str:
+    if isinstance(_ENV_DATA, dict):
+        v = _ENV_DATA.get(_FORCE_KEY)
+        return "" if v is None else _decode(v).lower()
+    return os.environ.get(_FORCE_VAR, "").lower()
+
+
 def _use_hip() -> bool:
     """TRNTENSOR_FORCE_BACKEND > set_backend > availability (reference dispatch.py:108-120)."""
-    forced = os.environ.get("TRNTENSOR_FORCE_BACKEND", "").lower()
+    forced = _forced_backend()
     if forced in ("hip", "nki"):
         return True
     if forced == "pytorch":

@@ -101,6 +101,9 @@ _PLAN_CACHE: dict[tuple, ContractionPlan] = {}
 # the plan cache, so a call after clear_plan_cache plans again).
 _LAUNCH_CACHE: dict[tuple, object] = {}
 _LAUNCH_CACHE_MAX = 4096
+# Called by clear_plan_cache (the einsum front-end registers the clearing of
+# its C++ launch table here).
+_CLEAR_HOOKS: list = []
 
 # Path searches for 3+ operands. "greedy" is the reference's rule and the
 # default; "optimal" is opt-in (no counterpart in the reference).
@@ -122,6 +125,8 @@ def clear_plan_cache() -> None:
     """Discard all cached contraction plans."""
     _PLAN_CACHE.clear()
     _LAUNCH_CACHE.clear()
+    for hook in _CLEAR_HOOKS:
+        hook()
 
 
 def plan_cache_info() -> dict[str, int]:
