@@ -719,6 +719,37 @@ class TestLaunchCache:
         trntensor.clear_plan_cache()
         assert len(E._fast) == 0
 
+    @pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+    def test_host_operands_repeat_bitwise(self, hip, dt):
+        """Small contiguous CPU operands: repeat calls are staged by the C++
+        table (one pinned upload, one launch, one download) and return CPU
+        tensors bitwise equal to the planned path's; non-contiguous and
+        large host operands are not recorded and stay on the planned path."""
+        E = importlib.import_module("trntensor_amd.einsum")
+        g = torch.Generator().manual_seed(7)
+        B = (torch.randn(8, 32, 96, generator=g) * 0.1).to(dt)
+        trntensor.clear_plan_cache()
+        first = trntensor.einsum("ap,bp->ab", B[0], B[1])
+        assert first.device.type == "cpu" and E._fast is not None and len(E._fast) == 1
+        for i, j, alpha in ((0, 1, 1.0), (2, 5, 2.5), (7, 7, 3)):
+            got = trntensor.einsum("ap,bp->ab", B[i], B[j], alpha=alpha)
+            planned = trntensor.einsum("ap,bp->ab", B[i], B[j], alpha=alpha, beta=0.0, out=torch.zeros(32, 32, dtype=dt))
+            assert got.device.type == "cpu" and got.dtype == dt and got.is_contiguous()
+            assert torch.equal(got, planned), (i, j, alpha)
+        want = cpu_ref.einsum("ap,bp->ab", B[0].double(), B[1].double())
+        assert normwise(first.double(), want) <= (1e-5 if dt == torch.float32 else 1e-12)
+        # 'bp,ap->ab' on the same operands runs swapped (the output is B^T A^T).
+        sw = trntensor.einsum("bp,ap->ab", B[3], B[4])
+        assert torch.equal(trntensor.einsum("bp,ap->ab", B[3], B[4]), sw) and len(E._fast) == 2
+        assert normwise(sw.double(), trntensor.einsum("ap,bp->ab", B[4], B[3]).double()) <= 1e-12
+        Bt = B.transpose(1, 2).contiguous().transpose(1, 2)  # non-contiguous views
+        n = len(E._fast)
+        nc = trntensor.einsum("ap,bp->ab", Bt[0], Bt[1])
+        assert len(E._fast) == n and torch.equal(trntensor.einsum("ap,bp->ab", Bt[0], Bt[1]), nc)
+        big = torch.randn(600, 1000, generator=g).to(dt)  # 2 x 4.8 MB operands: above the staging bound
+        trntensor.einsum("ik,jk->ij", big, big)
+        assert len(E._fast) == n
+
     def test_backend_switch_applies_to_cached_launches(self, hip):
         B = torch.randn(4, 32, 96).cuda()
         trntensor.einsum("ap,bp->ab", B[0], B[1])

@@ -115,7 +115,7 @@ def build_fastpath(verbose: bool = False) -> str:
         [os.path.join(HERE, "tt_fastpath.cpp")],
         build_directory=FASTPATH_DIR,
         extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include", f"-I{os.path.join(os.path.dirname(PKG), 'include')}"],
-        extra_ldflags=["-lc10_hip"],
+        extra_ldflags=["-lc10_hip", f"-L{rocm}/lib", "-lamdhip64"],
         with_cuda=False,
         verbose=verbose,
     )

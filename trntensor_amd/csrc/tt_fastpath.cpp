@@ -10,8 +10,13 @@
 // is passed in by address (no link dependency on libtrntensor_hip.so), so the
 // status codes map to the same exceptions as the ctypes path: TT_INVALID ->
 // ValueError, TT_UNSUPPORTED -> NotImplementedError, others -> RuntimeError.
+// Small contractions of contiguous host operands are recorded too: a repeat
+// call stages both operands through one pinned buffer and one upload, and
+// copies the result back before returning (run_host).
 #include <torch/extension.h>
+#include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 
 #include <cstring>
 #include <string>
@@ -34,7 +39,18 @@ struct Recipe {
     at::ScalarType dtype;
     c10::DeviceIndex device;
     bool swap;  // the output is computed as B^T A^T: operands exchanged
+    // Host operands (both contiguous, on the CPU): staged through one pinned
+    // buffer and one device buffer, the result copied back before returning.
+    bool host = false;
+    int64_t a_bytes = 0, b_bytes = 0, out_bytes = 0, b_off = 0;
 };
+
+constexpr int64_t kAlign = 256;
+// Largest host-operand contraction (both operands plus the output) staged
+// here; larger ones are bound by the copies and go through the planned path.
+constexpr int64_t kHostMaxBytes = int64_t(4) << 20;
+
+int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 void append(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
 
@@ -91,8 +107,41 @@ class LaunchTable {
         r.dtype = a.scalar_type();
         r.device = a.device().index();
         r.swap = swap;
-        if (map_.size() >= max_) map_.clear();
-        map_[make_key(sub, a, b)] = std::move(r);
+        insert(make_key(sub, a, b), std::move(r));
+    }
+
+    // Record the launch of (sub, a, b) for contiguous host operands: each call
+    // copies both into one pinned buffer, uploads it with one copy, launches
+    // on `device` and copies the output back, then waits for the stream.
+    // Returns false (nothing recorded) when the operands are not contiguous
+    // or the problem is above the staging bound.
+    bool add_host(const std::string& sub, const at::Tensor& a, const at::Tensor& b, const std::vector<int64_t>& params,
+                  const std::vector<int64_t>& sizes, bool swap, int64_t device) {
+        TORCH_CHECK(params.size() == kParams, "LaunchTable.add_host: ", kParams, " parameters expected");
+        TORCH_CHECK(a.device().is_cpu() && b.device().is_cpu() && a.scalar_type() == b.scalar_type(),
+                    "LaunchTable.add_host: host operands in one dtype expected");
+        if (!a.is_contiguous() || !b.is_contiguous()) return false;
+        Recipe r;
+        std::memcpy(r.params, params.data(), sizeof r.params);
+        r.sizes = sizes;
+        r.strides.assign(sizes.size(), 1);
+        int64_t acc = 1;
+        for (size_t d = sizes.size(); d-- > 0;) {
+            r.strides[d] = acc;
+            acc *= std::max<int64_t>(sizes[d], 1);
+        }
+        r.dtype = a.scalar_type();
+        r.device = static_cast<c10::DeviceIndex>(device);
+        r.swap = swap;
+        r.host = true;
+        const int64_t es = a.element_size();
+        r.a_bytes = a.numel() * es;
+        r.b_bytes = b.numel() * es;
+        r.out_bytes = acc * es;
+        r.b_off = round_up(r.a_bytes);
+        if (r.b_off + round_up(r.b_bytes) + r.out_bytes > kHostMaxBytes) return false;
+        insert(make_key(sub, a, b), std::move(r));
+        return true;
     }
 
     // alpha * (the recorded contraction of a and b), or None when (sub, a, b)
@@ -101,6 +150,7 @@ class LaunchTable {
         const auto it = map_.find(make_key(sub, a, b));
         if (it == map_.end()) return py::none();
         const Recipe& r = it->second;
+        if (r.host) return run_host(r, a, b, alpha);
         at::Tensor D = at::empty_strided(r.sizes, r.strides,
                                          at::TensorOptions().dtype(r.dtype).device(c10::DeviceType::CUDA, r.device));
         const at::Tensor& x = r.swap ? b : a;
@@ -115,6 +165,54 @@ class LaunchTable {
     size_t size() const { return map_.size(); }
 
    private:
+    void insert(std::string key, Recipe&& r) {
+        if (map_.size() >= max_) map_.clear();
+        map_[std::move(key)] = std::move(r);
+    }
+
+    // Host operands: one pinned staging buffer and one device buffer (held by
+    // the table, grown on demand up to kHostMaxBytes each) serve every call;
+    // each call waits for its stream before returning, so no two calls'
+    // copies overlap.
+    py::object run_host(const Recipe& r, const at::Tensor& a, const at::Tensor& b, double alpha) {
+        const int64_t in_bytes = r.b_off + r.b_bytes;
+        const int64_t out_off = round_up(in_bytes);
+        const int64_t total = out_off + r.out_bytes;
+        if (!pinned_.defined() || pinned_.numel() < total)
+            pinned_ = at::empty({total}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+        if (!dbuf_.defined() || dbuf_.numel() < total || dbuf_.device().index() != r.device)
+            dbuf_ = at::empty({total}, at::TensorOptions().dtype(at::kByte).device(c10::DeviceType::CUDA, r.device));
+        char* h = static_cast<char*>(pinned_.data_ptr());
+        char* d = static_cast<char*>(dbuf_.data_ptr());
+        std::memcpy(h, a.data_ptr(), r.a_bytes);
+        std::memcpy(h + r.b_off, b.data_ptr(), r.b_bytes);
+        c10::hip::HIPGuard guard(r.device);
+        hipStream_t st = c10::hip::getCurrentHIPStream(r.device).stream();
+        hip_check(hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, st), "hipMemcpyAsync (operands)");
+        const void* x = r.swap ? d + r.b_off : d;
+        const void* y = r.swap ? d : d + r.b_off;
+        const int rc = fn_(r.params, alpha, 0.0, x, y, nullptr, d + out_off, st);
+        if (rc != TT_OK) raise(rc);
+        hip_check(hipMemcpyAsync(h + out_off, d + out_off, r.out_bytes, hipMemcpyDeviceToHost, st),
+                  "hipMemcpyAsync (result)");
+        hipError_t e;
+        {
+            py::gil_scoped_release nogil;
+            e = hipStreamSynchronize(st);
+        }
+        hip_check(e, "hipStreamSynchronize");
+        at::Tensor D = at::empty_strided(r.sizes, r.strides, at::TensorOptions().dtype(r.dtype));
+        std::memcpy(D.data_ptr(), h + out_off, r.out_bytes);
+        return py::cast(D);
+    }
+
+    static void hip_check(hipError_t e, const char* what) {
+        if (e != hipSuccess) {
+            PyErr_SetString(PyExc_RuntimeError, (std::string("tt_gemm: ") + what + ": " + hipGetErrorString(e)).c_str());
+            throw py::error_already_set();
+        }
+    }
+
     [[noreturn]] void raise(int rc) const {
         const char* detail = err_();
         std::string msg = std::string("tt_gemm: ") + (detail && *detail ? detail : status_(rc));
@@ -130,6 +228,7 @@ class LaunchTable {
     status_fn status_;
     size_t max_;
     std::unordered_map<std::string, Recipe> map_;
+    at::Tensor pinned_, dbuf_;  // host-operand staging
 };
 
 }  // namespace
@@ -140,6 +239,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         .def(py::init<int64_t, int64_t, int64_t, int64_t>(), py::arg("packed"), py::arg("last_error"),
              py::arg("status_string"), py::arg("max_entries"))
         .def("add", &LaunchTable::add)
+        .def("add_host", &LaunchTable::add_host)
         .def("run", &LaunchTable::run)
         .def("clear", &LaunchTable::clear)
         .def("__len__", &LaunchTable::size);

@@ -128,11 +128,15 @@ def _clear_launches() -> None:
 
 def _remember_launch(subscripts, plan, a, b) -> None:
     """Record the launch of a just-run two-operand contraction when both
-    operands are on one HIP device in one real dtype and the engine ran it
-    as one in-place GEMM launch (its recipe is cached)."""
+    operands are on one HIP device (or both on the host) in one real dtype
+    and the engine ran it as one in-place GEMM launch (its recipe is
+    cached). Host operands are recorded only in the C++ table, which stages
+    small contiguous ones through pinned memory."""
     global _fast
-    if (plan.strategy == "path" or a.device.type != "cuda" or b.device != a.device or a.dtype != b.dtype
-            or a.dtype not in _FAST_DTYPES or _PLAN_CACHE.get(_shape_key(subscripts, (a, b))) is not plan):
+    host = a.device.type == "cpu" and b.device.type == "cpu"
+    if (plan.strategy == "path" or not (host or a.device.type == "cuda") or b.device != a.device
+            or a.dtype != b.dtype or a.dtype not in _FAST_DTYPES
+            or _PLAN_CACHE.get(_shape_key(subscripts, (a, b))) is not plan):
         return
     lhs, out_str = _parse_subscripts(subscripts)
     ta, tb = lhs.split(",")
@@ -147,7 +151,12 @@ def _remember_launch(subscripts, plan, a, b) -> None:
     if _fast is not None:
         params = rec.packed_params()
         if params is not None:
-            _fast.add(subscripts, a, b, params, list(rec.shape), bool(rec.swap))
+            if host:
+                _fast.add_host(subscripts, a, b, params, list(rec.shape), bool(rec.swap), dispatch._device().index or 0)
+            else:
+                _fast.add(subscripts, a, b, params, list(rec.shape), bool(rec.swap))
+        return
+    if host:
         return
     run = rec.launcher(a.device)
     if run is not None:
