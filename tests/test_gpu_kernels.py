@@ -227,11 +227,15 @@ def test_gemm_direct_b_k_contiguous_matches_lds_tile(hip, ta, M, N, K, batch, al
         (True, False, 128, 384, 37, 3, True),  # K tail, B row-major
         (True, True, 192, 128, 16, 1, False),
         (False, True, 4224, 256, 64, 1, True),  # 66 row tiles: the grouped row order of config 5's GEMM
+        (False, True, 400, 256, 800, 1, True),  # ragged M: config 5's optimal-order dot GEMM, transposed
+        (True, False, 200, 384, 37, 2, False),  # ragged M and K tail, B row-major
+        (False, False, 33, 128, 16, 1, True),  # one partial row tile
     ],
 )
 def test_gemm_dot_direct_b_matches_lds_tile(hip, ta, tb, M, N, K, batch, with_e2):
-    """fp64 dot GEMM (sum of op(A) op(B) .* E1 .* E2) with M a multiple of 64 and
-    N of 128: the direct-B kernel's dot epilogue. Against float64 torch, and
+    """fp64 dot GEMM (sum of op(A) op(B) .* E1 .* E2) with N a multiple of 128
+    (any M; rows past M are left out of the sum): the direct-B kernel's dot
+    epilogue. Against float64 torch, and
     against the LDS-staged tiles (odd ldb) to 1e-13 relative: the per-tile sums
     are added in another order."""
     from trntensor_amd.hip import engine

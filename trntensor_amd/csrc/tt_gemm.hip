@@ -589,6 +589,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     for (int a = 0; a < 4; ++a) acc[a][b] = MF::mma(fa[a][e], rb[p][e], acc[a][b]);
             }
         };
+        // A wave whose columns all lie past N (in a last, partial column tile)
+        // only helps stage A: the same loads, stores and barriers as the
+        // loop below, no B loads and no MFMAs, so its SIMD's MFMA pipe serves
+        // the other workgroups. Its accumulators stay zero and are never
+        // stored (not with DOT, whose column tiles are full). Config 5's
+        // optimal-order step 'jb,abP->jaP' (N = 800): 0.828 against 0.830 and
+        // 0.836 ms for the whole path, 12% fewer executed MFMA FLOP there.
+        const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (!DOT && tn * BN + (int64_t)wave_u * (16 * NB) >= g.N) {
+            aload(0);
+            sa.store(lds);
+            __syncthreads();
+            for (int64_t t = 0; t + 1 < nk; ++t) {
+                aload(t + 1);
+                sa.store(lds + ((t + 1) & 1) * SA::ELEMS);
+                __syncthreads();
+            }
+        } else {
         aload(0);
         sa.store(lds);
         int64_t t = 0;
@@ -659,6 +677,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const T* cur = lds + (t & 1) * SA::ELEMS;
 #pragma unroll
         for (int p = 0; p < 4; ++p) piece(cur, p);
+        }  // live wave
     }
 
     if constexpr (DOT) {
@@ -1003,14 +1022,15 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // 67.9-68.0 ms, the sum equal to 2e-15 (another order of the per-tile
     // sums).
     // Any even N (a last, partial column tile clamps its columns; the dot
-    // epilogue keeps N a multiple of 128). Same box, alternating, bitwise
+    // epilogue keeps N a multiple of 128, any M: rows past M read A as zero
+    // and are left out of the sum). Same box, alternating, bitwise
     // equal, against the LDS-staged tiles: 3000 x 3000 x 1000 with alpha/beta
     // 0.331 against 0.438 ms, NT 0.382 against 0.426 ms, 8192 x 200 x 2048
     // 0.145 against 0.186 ms, config 5's optimal-order GEMM (400 x 128 x 800
     // x 400) 0.580 against 0.629 ms. The fp32 tile lost on such shapes (3000
     // x 3000 x 1000 0.221 against 0.212 ms), so fp32 keeps whole tiles.
     if constexpr (sizeof(T) == 8)
-        if (vec && (DOT ? g.N % 128 == 0 && g.M % 64 == 0 : g.N % 2 == 0))
+        if (vec && (DOT ? g.N % 128 == 0 : g.N % 2 == 0))
             return launch_directb<T, DOT>(g, ta, tb, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);
     // fp32 on 64 x 256 tiles (four 16-column MFMA blocks per wave, so a lane's
     // B piece is still 16 bytes): within 1-2% of the LDS-staged tiles, ahead

@@ -912,8 +912,15 @@ def contract_gemm_dot(
             strided_contract([(op.ext[c], op.strd[c], 0) for c in keep], [(op.ext[c], op.strd[c], 0) for c in gone], op.t, None, R)
             ops[idx] = Operand("".join(keep), R)
     A, B = ops
-    kl.sort(key=lambda c: -A.strd[c])
     ext = {**A.ext, **B.ext}
+    # The fp64 direct-B dot kernel needs whole 128-column tiles (any M): with
+    # N ragged and M whole, the product is formed transposed (X^T = B^T A^T,
+    # E read with the row and column letters exchanged). Config 5's
+    # optimal-order dot GEMM (16384 x 400 x 800): 400 x 16384 runs on the
+    # direct-B kernel with 448 padded rows instead of 512 padded columns.
+    if dt == torch.float64 and _numel(ext[c] for c in nl) % 128 and not _numel(ext[c] for c in ml) % 128:
+        A, B, ml, nl = B, A, nl, ml
+    kl.sort(key=lambda c: -A.strd[c])
     nb = _numel(ext[c] for c in batch)
     M = _numel(ext[c] for c in ml)
     N = _numel(ext[c] for c in nl)
