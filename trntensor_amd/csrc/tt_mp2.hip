@@ -293,6 +293,22 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     for (; kt + 1 < nfull; ++kt) {
         load((kt + 1) * BK, std::true_type{});
         compute(0, (kt + 1) * BK, 1);
+        if constexpr (DQ && sizeof(T) == 4) {
+            // fp32: one of the stage's four loads (two staged panels, then
+            // the two column fragments) after every 8 MFMAs; left alone the
+            // compiler bunched all four after the 28th. Config 4 fp32, same
+            // box, alternating, bitwise equal: 3.900-3.913 against 3.942-3.970
+            // ms (nvir 300: 4.91 against 5.01 ms). The staged panels' loads
+            // after the 4th and 8th MFMA instead: 4.11-4.13 ms; the same
+            // spacing in fp64 (eight loads): -0.6% at naux 1200, +0.7% at 2400.
+            constexpr int NL = 4 * PN::NP;  // loads per thread per stage
+            constexpr int NM = 8 * KS;      // MFMAs per wave per stage
+#pragma unroll
+            for (int l = 0; l < NL; ++l) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NM / NL, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         store(0);
