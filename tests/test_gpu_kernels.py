@@ -95,6 +95,8 @@ def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
         (False, True, 300, 50, 90, 1),  # 256 x 64 tiles (N <= 64)
         (True, True, 257, 300, 129, 1),  # 64 x 128 tiles (small grid), ragged edges
         (False, True, 2700, 2700, 40, 1),  # 128 x 128 tiles (484 of them), ragged edges
+        (False, False, 200, 512, 48, 2),  # direct-B, 16-byte C pieces of two row blocks at a time, ragged M
+        (True, False, 512, 768, 64, 3),  # direct-B, the batched shape family of config 2
     ],
 )
 def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):

@@ -423,6 +423,46 @@ __device__ __forceinline__ void directb_store(const GemmArgs& g, typename Mfma<T
     const bool vecd = ((reinterpret_cast<uintptr_t>(D) | (uintptr_t)(g.ldd * sizeof(T))) & 15) == 0 &&
                       (!C || ((reinterpret_cast<uintptr_t>(C) | (uintptr_t)(g.ldc * sizeof(T))) & 15) == 0);
     const bool colok = col < g.N;  // N is a multiple of NB: all NB columns or none
+    if (C && vecd) {
+        // A lane's NB columns of a row are one 16-byte piece of C and of D.
+        // The C pieces of two row blocks (eight rows) go out together before
+        // their stores: two memory round trips per tile instead of four, and
+        // one load per row instead of NB. D may alias C exactly: every row's
+        // C piece is loaded before that row's store. Same box, alternating,
+        // bitwise equal: 64 x 512^3 with alpha/beta and C 0.1362-0.1366
+        // against 0.1429-0.1432 ms fp32, 0.2615-0.2618 against 0.2646-0.2661
+        // ms fp64; 4096^3 fp32 0.993 against 0.999 ms.
+#pragma unroll
+        for (int a2 = 0; a2 < 4; a2 += 2) {
+            v16_t cv[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + 16 * (a2 + h) + MF::row(lg, r);
+                    const bool ok = (FULLM || row < g.M) && colok;
+                    const v16_t x = *reinterpret_cast<const v16_t*>(C + (ok ? row * g.ldc + col : 0));
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) cv[h][r][b] = ok ? x[b] : T(0);
+                }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + 16 * (a2 + h) + MF::row(lg, r);
+                    if ((!FULLM && row >= g.M) || !colok) continue;
+                    v16_t v;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        v[b] = acc[a2 + h][b][r];
+                        if (g.alpha != 1.0) v[b] = alpha * v[b];
+                        v[b] = v[b] + beta * cv[h][r][b];
+                    }
+                    *reinterpret_cast<v16_t*>(D + row * g.ldd + col) = v;
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
         T cv[4][NB];
