@@ -73,17 +73,16 @@ struct Panel {
         for (int e = 0; e < AW; ++e) reg[c * AW + e] = x[e];
     }
 
-    // FAST (interior stage: all 64 rows present, BK k in range): NP
-    // unconditional loads. Otherwise (a block with fewer than 64 rows, or
-    // the K tail) each AW-piece is one load when it lies inside, zero
-    // without a load when it lies outside, and element loads from clamped
-    // addresses only when it straddles the end of the row. Element loads
-    // throughout made every unit of a ragged block slow: nocc 64, nvir 300,
-    // naux 1200 took 8.99 ms (fp64) and 6.22 ms (fp32) against 8.38 and
-    // 4.54 ms this way.
+    // FAST (interior stage: BK k in range): NP unconditional loads; in a
+    // block with fewer than 64 rows the rows past its end read its last row
+    // again (their products are never used: the energy loop skips rows and
+    // columns past the block). Otherwise (the K tail) each AW-piece is one
+    // load when it lies inside, zero without a load when it lies outside,
+    // and element loads from clamped addresses only when it straddles the
+    // end of the row.
     template <bool FAST>
     __device__ __forceinline__ void load(const T* __restrict__ base, int rows, int64_t naux, int64_t k0) {
-        const int r = threadIdx.x >> 2;
+        const int r = FAST ? min((int)(threadIdx.x >> 2), rows - 1) : (int)(threadIdx.x >> 2);
         const int k = (threadIdx.x & 3) * E;
         const T* row = base + (int64_t)r * naux;
         if (FAST) {
@@ -160,8 +159,11 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     const int wr = (wave >> 1) * 32;
     const int wc = (wave & 1) * 32;
     const int64_t nk = (naux + BK - 1) / BK;
-    // Stages 0 .. nfull-1 are interior (all rows present, all BK k in range).
-    const int64_t nfull = (rows_p == kMp2Tile && rows_q == kMp2Tile) ? naux / BK : 0;
+    // Stages 0 .. nfull-1 are interior (all BK k in range). Ragged blocks (fewer than 64 rows) take this loop too, their missing
+    // rows reading the block's last row: config 4's shape with nvir 300
+    // (44-row last block) ran 5.0 ms fp32 with those units in the guarded
+    // loop.
+    const int64_t nfull = naux / BK;
 
     // DQ (with Y): each wave's two column fragments (B_j[q] for the X
     // waves, B_i[q] for the Y waves) go from memory straight into registers: a
@@ -187,7 +189,7 @@ __device__ __forceinline__ void mp2_kloop(T* lds_base, const T* base0, const T* 
     typename PN::vec_t fq[2];
     auto qload = [&](int b, int64_t k0, auto fast) __attribute__((always_inline)) {
         constexpr bool F = decltype(fast)::value;
-        const int r = qch + 16 * b + (lane & 15);
+        const int r = F ? min(qch + 16 * b + (lane & 15), rows_q - 1) : qch + 16 * b + (lane & 15);
         const int64_t k = k0 + PN::E * (lane >> 4);
         const T* row = qbase + (int64_t)r * naux;
 #pragma unroll
