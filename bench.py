@@ -561,7 +561,8 @@ def bench_c4_naux(torch, tt, dev, args):
     """Config 4 with auxiliary sizes that are not multiples of 16 (real
     auxiliary basis sizes are arbitrary). Each call (timed whole) first copies
     B into the workspace with rows padded to a multiple of 16 elements, so
-    every stage of the kernel reads aligned cache lines."""
+    every stage of the kernel reads aligned cache lines. Also nvir 300 (not a
+    multiple of the 64-row block) and a problem past the MALL."""
     out = {}
     for dt, key, peak in ((torch.float64, "f64", PEAK["f64"]), (torch.float32, "f32", PEAK["f32"])):
         for naux in (1200, 1190, 1199, 1201):
@@ -572,6 +573,16 @@ def bench_c4_naux(torch, tt, dev, args):
             out[f"{key}_naux{naux}"] = {"ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                                         "frac_mfma": round(flop / (ms * 1e-3) / peak, 4)}
             del B, eo, ev
+        # nvir not a multiple of the 64-row block (a 44-row last block): the
+        # fraction counts algorithmic FLOP only, so the padded rows' work is
+        # overhead here.
+        print(f"bench: c4 nvir 300 {key}", file=sys.stderr, flush=True)
+        B, eo, ev = (x.to(dev) for x in mp2_inputs(torch, dt, nvir=300))
+        _, ms = timed_steady(torch, lambda: tt.mp2_energy(B, eo, ev), max(5, args.steps))
+        flop = 2080 * 2 * 300**2 * 1200
+        out[f"{key}_nvir300"] = {"ms": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+                                 "frac_mfma": round(flop / (ms * 1e-3) / peak, 4)}
+        del B, eo, ev
     # A production-sized problem whose B (1.57 GB) does not fit the 256 MB
     # MALL, so the panel re-reads that miss L2 go to HBM (inputs drawn on the
     # device; same distributions as config 4).
