@@ -97,6 +97,7 @@ def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
         (False, True, 2700, 2700, 40, 1),  # 128 x 128 tiles (484 of them), ragged edges
         (False, False, 200, 512, 48, 2),  # direct-B, 16-byte C pieces of two row blocks at a time, ragged M
         (True, False, 512, 768, 64, 3),  # direct-B, the batched shape family of config 2
+        (False, False, 4096, 4096, 96, 1),  # fp32: the 256 x 256 LDS tile, three stages
     ],
 )
 def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
@@ -129,13 +130,18 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
         # more than 64 row tiles: rows in groups of 16 slabs sweeping every column tile
         (False, 4160, 512, 48, 1, 1.5, 0.5, True, 0),
         (True, 4200, 768, 40, 2, 1.0, 0.0, False, 1),  # ragged last group and rows
+        # fp32, whole 256 x 256 tiles, one per CU: the LDS-staged 256 x 256 tile kernel
+        (False, 4096, 4096, 64, 1, 1.5, 0.5, True, 0),
+        (False, 2048, 8192, 32, 1, 1.0, 0.0, False, 0),  # one 32-k stage
     ],
 )
 def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):
     """B row-major, N even (fp64) or a multiple of 256 (fp32): the kernel that
-    loads B straight into the MFMA registers. Checked against float64 torch,
-    and bitwise against the LDS-staged tiles, which the same problem takes when
-    B's leading dimension breaks 16-byte alignment (no vector path)."""
+    loads B straight into the MFMA registers, or, for fp32 problems of whole
+    256 x 256 tiles filling the chip, the 256 x 256 tile. Checked against
+    float64 torch, and bitwise against the LDS-staged tiles, which the same
+    problem takes when B's leading dimension breaks 16-byte alignment (no
+    vector path)."""
     from trntensor_amd.hip import engine
 
     g = torch.Generator().manual_seed(M + N + K + batch + int(ta))

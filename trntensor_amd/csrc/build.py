@@ -28,6 +28,7 @@ SOURCES = [
     "tt_gemm.hip",
     "tt_gemm16.hip",
     "tt_gemm16_dma.hip",
+    "tt_gemm_big.hip",
     "tt_mp2.hip",
     "tt_probe.hip",
     "tt_strided.hip",

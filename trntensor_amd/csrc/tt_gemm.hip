@@ -1077,6 +1077,20 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // on short K (same box, alternating, bitwise equal: 4096^2 x 512 0.1345
     // against 0.1364 ms, 64 x 512^3 with alpha/beta and C 0.1397 against
     // 0.1414 ms, 4096^3 0.988 against 0.990 ms).
+    // fp32, both operands not transposed, whole 256 x 256 tiles in whole
+    // rounds of one tile per CU (at least 95% of the last round busy): the
+    // 256 x 256 LDS tile (tt_gemm_big.hip), bitwise equal to the tiles
+    // below. Same box, alternating: 4096^3 with alpha/beta and C 0.968
+    // against 0.996 ms, without C 0.963 against 0.998; 8192^2 x 2048 1.930
+    // against 1.969; 2048 x 8192 x 4096 0.971 against 1.005 ms; 4096^2 x 1024
+    // 0.253 against 0.258 ms. A partial last round loses: 6144^2 x 2048 (2.25
+    // rounds) 1.444 against 1.118 ms, 5120^2 x 2048 0.961 against 0.869 ms.
+    if constexpr (sizeof(T) == 4 && !DOT)
+        if (gemm_big_f32_fits(ta, tb, g)) {
+            const int64_t tiles = (g.M / 256) * (g.N / 256), cus = device_cus();
+            const int64_t rounds = (tiles + cus - 1) / cus;
+            if (tiles >= cus && 100 * tiles >= 95 * rounds * cus) return gemm_big_f32_launch(g, st);
+        }
     if constexpr (sizeof(T) == 4 && !DOT)
         if (!tb && vec && g.N % 256 == 0)
             return launch_directb<T, DOT>(g, ta, false, g.M <= 64 && (g.batch == 1 || g.sB != 0), st);

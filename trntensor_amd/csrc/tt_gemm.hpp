@@ -41,6 +41,10 @@ int gemm16_dma_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st
 int gemm16_dma_rows(bool ta, bool tb, int64_t K);
 // Its tile (bm x bn) for an M x N x K problem of `batch` products.
 void gemm16_dma_tile(bool ta, bool tb, int64_t M, int64_t N, int64_t K, int64_t batch, int& bm, int& bn);
+// fp32 on 256 x 256 tiles (tt_gemm_big.hip): whether it takes the problem,
+// and its launch.
+bool gemm_big_f32_fits(bool ta, bool tb, const GemmArgs& g);
+int gemm_big_f32_launch(GemmArgs& g, hipStream_t st);
 // Dot epilogue; writes one double per workgroup to g.partial and returns the
 // number of workgroups in *nparts.
 int gemm_dot_dispatch(int dtype, bool ta, bool tb, GemmArgs& g, hipStream_t st, int64_t* nparts);
