@@ -4,7 +4,7 @@
 // tile per CU).
 //
 // Eight waves of 64 x 128 (4 x 8 blocks of v_mfma_f32_16x16x4f32, 128 fp32
-// accumulators per lane), two waves per SIMD, one workgroup per CU (140 KB
+// accumulators per lane), two waves per SIMD, one workgroup per CU (144 KiB
 // of LDS). Stages of 32 k, double-buffered, one barrier per stage. The next
 // stage's global loads are spread over the stage's first 16-k chunk (one per
 // 16 MFMAs) and its LDS stores over the second (into the other buffer, which
@@ -12,7 +12,10 @@
 // 64 x 256 tiles at four workgroups per CU (same box, alternating): 4096^3
 // fp32 0.968 against 0.996 ms; the template's other shape, 128 x 256 tiles
 // with 16-k stages at two workgroups per CU, 0.996 ms; B read one MFMA step
-// ahead, 0.977 ms.
+// ahead, 0.977 ms. LDS pitches (floats of padding per A row / B k-row, 4096^3
+// fraction of the fp32 peak, one box): 8 / 0 0.914, 4 / 0 0.908, 12 / 0
+// 0.908, 4 / 4 0.900, 4 / 16 0.909, 8 / 8 0.892, unpadded A 0.882; A pieces
+// XOR-swizzled instead of padded 0.898.
 //
 // Fragments (the layout of gemm_directb_kernel, whose results this kernel
 // reproduces bitwise): chunk h of a stage is 16 k; MFMA step p of chunk h
@@ -37,8 +40,8 @@ struct BigCfg {
     static constexpr int NW = TM / 64 * 2;  // waves
     static constexpr int T = 64 * NW;       // threads
     static constexpr int CH = BK / 16;      // 16-k chunks per stage
-    static constexpr int AP = BK + 4;       // floats per A row in LDS
-    static constexpr int BP = kBigN + 4;    // floats per B k-row in LDS
+    static constexpr int AP = BK + 8;       // floats per A row in LDS
+    static constexpr int BP = kBigN;        // floats per B k-row in LDS (unpadded)
     static constexpr int AE = TM * AP;      // A floats per stage buffer
     static constexpr int BE = BK * BP;      // B floats per stage buffer
     static constexpr int LA = BK / 4;       // threads per A row (16 bytes each)
