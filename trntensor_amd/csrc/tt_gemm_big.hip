@@ -6,9 +6,10 @@
 // Eight waves of 64 x 128 (4 x 8 blocks of v_mfma_f32_16x16x4f32, 128 fp32
 // accumulators per lane), two waves per SIMD, one workgroup per CU (144 KiB
 // of LDS). Stages of 32 k, double-buffered, one barrier per stage. The next
-// stage's global loads are spread over the stage's first 16-k chunk (one per
-// 16 MFMAs) and its LDS stores over the second (into the other buffer, which
-// the previous barrier released). Measured against the direct-B kernel's
+// stage's global loads are spread over the first half of the stage's first
+// 16-k chunk (one per 8 MFMAs; one per 16: -0.5 points, per 4 or all first:
+// -0.4) and its LDS stores over the second chunk (one per 16 MFMAs, into the
+// other buffer, which the previous barrier released). Measured against the direct-B kernel's
 // 64 x 256 tiles at four workgroups per CU (same box, alternating): 4096^3
 // fp32 0.968 against 0.996 ms; the template's other shape, 128 x 256 tiles
 // with 16-k stages at two workgroups per CU, 0.996 ms; B read one MFMA step
@@ -169,7 +170,7 @@ void gemm_big_f32_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_barrier(0);
         } else {
             chunk(buf, 0);
-            spread_loads(FULL);
+            spread_loads(HALF);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int h = 1; h + 1 < CH; ++h) chunk(buf, h);
