@@ -35,7 +35,7 @@ SOURCES = [
 ]
 # Sources whose MFMA accumulators belong in AGPRs (256 fp32 per lane): built
 # without the VGPR-accumulator option below.
-AGPR_SOURCES = {"tt_gemm16_dma.hip"}
+AGPR_SOURCES = {"tt_gemm16_dma.hip", "tt_gemm_big.hip"}
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

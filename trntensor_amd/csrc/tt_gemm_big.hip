@@ -3,20 +3,29 @@
 // of 32, 16-byte aligned; the dispatcher takes it in whole rounds of one
 // tile per CU).
 //
-// Eight waves of 64 x 128 (4 x 8 blocks of v_mfma_f32_16x16x4f32, 128 fp32
-// accumulators per lane), two waves per SIMD, one workgroup per CU (144 KiB
-// of LDS). Stages of 32 k, double-buffered, one barrier per stage. The next
-// stage's global loads are spread over the first half of the stage's first
-// 16-k chunk (one per 8 MFMAs; one per 16: -0.5 points, per 4 or all first:
-// -0.4) and its LDS stores over the second chunk (one per 16 MFMAs, into the
-// other buffer, which the previous barrier released). Measured against the direct-B kernel's
-// 64 x 256 tiles at four workgroups per CU (same box, alternating): 4096^3
-// fp32 0.968 against 0.996 ms; the template's other shape, 128 x 256 tiles
-// with 16-k stages at two workgroups per CU, 0.996 ms; B read one MFMA step
-// ahead, 0.977 ms. LDS pitches (floats of padding per A row / B k-row, 4096^3
-// fraction of the fp32 peak, one box): 8 / 0 0.914, 4 / 0 0.908, 12 / 0
-// 0.908, 4 / 4 0.900, 4 / 16 0.909, 8 / 8 0.892, unpadded A 0.882; A pieces
-// XOR-swizzled instead of padded 0.898.
+// Four waves of 128 x 128 (8 x 8 blocks of v_mfma_f32_16x16x4f32), one wave
+// per SIMD, one workgroup per CU (144 KiB of LDS). The 256 fp32 accumulators
+// per lane live in AGPRs: this file is built without the VGPR-accumulator
+// option the other kernels use, which leaves the wave its 256 VGPRs for two
+// sets of fragments and the staging registers.
+//
+// Stages of 32 k (two 16-k chunks), double-buffered in LDS, one barrier per
+// stage; A rows padded by 8 floats, B k-rows unpadded (no LDS bank conflicts;
+// B k-rows padded by 4 floats conflicted in 3/8 of the LDS-active cycles).
+// With one wave per SIMD nothing else covers a stall, so the loop is
+// software-pipelined and every memory instruction is spread among the MFMAs:
+//  - chunk 0's MFMAs run with chunk 1's fragment reads and the next stage's
+//    global loads interleaved, one of each per 16 MFMAs;
+//  - chunk 1's first three MFMA steps run with the next stage's LDS stores
+//    (into the other buffer, which the previous barrier released), one per
+//    12 MFMAs;
+//  - the barrier comes before chunk 1's last step, whose 64 MFMAs run with
+//    the next stage's chunk-0 fragment reads, one per 4 MFMAs.
+// Same box, alternating, fraction of the fp32 peak: 4096^3 0.933, 8192^2 x
+// 2048 0.934, 2048 x 8192 x 4096 0.929, 4096^2 x 1024 0.892, against 0.920,
+// 0.924, 0.919, 0.876 for eight waves of 64 x 128 at two waves per SIMD
+// (accumulators in VGPRs, no room for a second fragment set) and 0.88 or
+// less for the 64 x 256 direct-B tiles.
 //
 // Fragments (the layout of gemm_directb_kernel, whose results this kernel
 // reproduces bitwise): chunk h of a stage is 16 k; MFMA step p of chunk h
@@ -25,44 +34,28 @@
 // 16-byte LDS read feeds steps 0..3); its B operand piece for step p is four
 // consecutive columns 4 (lane % 16) .. + 3 of one k-row (one 16-byte read),
 // one column for each of the four MFMA column blocks of a 64-column set.
-#include <type_traits>
-
 #include "tt_gemm.hpp"
 
 namespace tt {
 
 namespace {
 
-constexpr int kBigN = 256;
 typedef float f4_v __attribute__((ext_vector_type(4)));
 
-template <int TM, int BK>
-struct BigCfg {
-    static constexpr int NW = TM / 64 * 2;  // waves
-    static constexpr int T = 64 * NW;       // threads
-    static constexpr int CH = BK / 16;      // 16-k chunks per stage
-    static constexpr int AP = BK + 8;       // floats per A row in LDS
-    static constexpr int BP = kBigN;        // floats per B k-row in LDS (unpadded)
-    static constexpr int AE = TM * AP;      // A floats per stage buffer
-    static constexpr int BE = BK * BP;      // B floats per stage buffer
-    static constexpr int LA = BK / 4;       // threads per A row (16 bytes each)
-    static constexpr int RA = TM * LA / T;  // A loads per thread per stage
-    static constexpr int RB = BK * 64 / T;  // B loads per thread per stage (64 threads per k-row)
-    static constexpr int NL = RA + RB;
-    static constexpr int WG_PER_CU = TM == 256 ? 1 : 2;
-    static_assert(RA >= 1 && RB >= 1 && TM * LA % T == 0 && BK * 64 % T == 0, "staging split");
-};
+constexpr int kBigM = 256, kBigN = 256, kBigK = 32;  // tile and stage
+constexpr int kBigThreads = 256;
 
-constexpr int big_threads(int tm) { return tm / 64 * 2 * 64; }
-constexpr int big_wgs_per_cu(int tm) { return tm == 256 ? 1 : 2; }
-
-template <int TM, int BK>
-__global__ __launch_bounds__(big_threads(TM), big_wgs_per_cu(TM)) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_big_f32_kernel(GemmArgs g) {
-    typedef BigCfg<TM, BK> C_;
-    constexpr int T = C_::T, AP = C_::AP, BP = C_::BP, AE = C_::AE, BE = C_::BE, LA = C_::LA, RA = C_::RA, RB = C_::RB,
-                  NL = C_::NL, CH = C_::CH;
-    constexpr int MC = 4 * 8 * 4;  // MFMAs per wave per chunk
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_big_f32_kernel(GemmArgs g) {
+    constexpr int T = kBigThreads, BK = kBigK;
+    constexpr int AP = BK + 8;          // floats per A row in LDS
+    constexpr int BP = kBigN;           // floats per B k-row in LDS
+    constexpr int AE = kBigM * AP;      // A floats per stage buffer
+    constexpr int BE = BK * BP;         // B floats per stage buffer
+    constexpr int LA = BK / 4;          // threads per A row (16 bytes each)
+    constexpr int RA = kBigM * LA / T;  // A loads per thread per stage
+    constexpr int RB = BK * 64 / T;     // B loads per thread per stage (64 threads per k-row)
+    constexpr int NL = RA + RB;
+    static_assert(NL == 16, "the schedule below spreads 16 loads, stores and fragment reads");
     __shared__ __attribute__((aligned(16))) float lds[2 * (AE + BE)];
 
     // Rows of tiles in groups of four, each group column-major: an XCD's
@@ -73,7 +66,7 @@ void gemm_big_f32_kernel(GemmArgs g) {
     const int64_t gm = min((int64_t)4, g.tiles_m - grp * 4);
     const int64_t rr = id - grp * 4 * g.tiles_n;
     const int64_t tn = rr / gm, tm = grp * 4 + rr % gm;
-    const int64_t m0 = tm * TM, n0 = tn * kBigN;
+    const int64_t m0 = tm * kBigM, n0 = tn * kBigN;
     const float* A = static_cast<const float*>(g.A);
     const float* B = static_cast<const float*>(g.B);
 
@@ -81,7 +74,7 @@ void gemm_big_f32_kernel(GemmArgs g) {
     const int lane = t & 63;
     const int w = t >> 6;
     const int lg = lane >> 4, c = lane & 15;
-    const int wm = w >> 1, wn = w & 1;  // rows 64 wm .., columns 128 wn ..
+    const int wm = w >> 1, wn = w & 1;  // rows 128 wm .., columns 128 wn ..
 
     // Global -> registers: A rows t / LA + (T / LA) i, k (t % LA) 4; B k-rows
     // t / 64 + (T / 64) i, columns (t % 64) 4. Every instruction covers whole
@@ -105,87 +98,84 @@ void gemm_big_f32_kernel(GemmArgs g) {
         for (int i = 0; i < RB; ++i)
             *reinterpret_cast<f4_v*>(bs + ((t >> 6) + (T / 64) * i) * BP + (t & 63) * 4) = rb[i];
     };
-
-    f4_v acc[4][8];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[a][j] = f4_v{0, 0, 0, 0};
-
-    auto chunk = [&](int buf, int h) __attribute__((always_inline)) {
+    // Chunk h's fragments of stage buffer buf: eight A pieces, then the B
+    // pieces of both 64-column sets for steps 0..3.
+    auto reads = [&](int buf, int h, f4_v (&fa)[8], f4_v (&fb)[2][4]) __attribute__((always_inline)) {
         const float* as = lds + buf * (AE + BE);
         const float* bs = as + AE;
-        f4_v fa[4], fb[2][4];
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
-            fa[a] = *reinterpret_cast<const f4_v*>(as + (64 * wm + 16 * a + c) * AP + 16 * h + 4 * lg);
+        for (int a = 0; a < 8; ++a)
+            fa[a] = *reinterpret_cast<const f4_v*>(as + (128 * wm + 16 * a + c) * AP + 16 * h + 4 * lg);
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int p = 0; p < 4; ++p)
                 fb[s][p] = *reinterpret_cast<const f4_v*>(bs + (16 * h + 4 * lg + p) * BP + 128 * wn + 64 * s + 4 * c);
+    };
+
+    f4_v acc[8][8];
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
+    for (int a = 0; a < 8; ++a)
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+        for (int j = 0; j < 8; ++j) acc[a][j] = f4_v{0, 0, 0, 0};
+    // MFMA steps p0 .. p1 - 1 of one chunk: 64 MFMAs per step.
+    auto mfma = [&](const f4_v (&fa)[8], const f4_v (&fb)[2][4], int p0, int p1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = p0; p < p1; ++p)
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
 #pragma unroll
                     for (int b = 0; b < 4; ++b)
-                        acc[a][4 * s + b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a][p], fb[s][p][b],
-                                                                                 acc[a][4 * s + b], 0, 0, 0);
+                        acc[a][4 * s + b] =
+                            __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a][p], fb[s][p][b], acc[a][4 * s + b], 0, 0, 0);
     };
-    // Scheduling of a stage's loads (mask 0x020) and stores (0x200) among
-    // MFMAs (0x008).
-    auto spread_loads = [&](auto per) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, decltype(per)::value, 0);
-        }
-    };
-    auto spread_stores = [&](auto per) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, decltype(per)::value, 0);
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-        }
-    };
-    constexpr std::integral_constant<int, MC / 2 / NL> HALF{};
-    constexpr std::integral_constant<int, MC / NL> FULL{};
 
+    // Scheduling-group masks: 0x008 MFMA, 0x020 global load, 0x100 LDS read,
+    // 0x200 LDS write.
+    f4_v fa0[8], fb0[2][4], fa1[8], fb1[2][4];
     const int64_t nk = g.K / BK;
     gload(0);
     sstore(0);
     __syncthreads();
+    reads(0, 0, fa0, fb0);
     int64_t st = 0;
     for (; st + 1 < nk; ++st) {
         const int buf = (int)(st & 1);
+        reads(buf, 1, fa1, fb1);
         gload((st + 1) * BK);
-        if constexpr (CH == 1) {
-            chunk(buf, 0);
-            sstore(buf ^ 1);
-            spread_loads(HALF);
-            spread_stores(HALF);
-            __builtin_amdgcn_sched_barrier(0);
-        } else {
-            chunk(buf, 0);
-            spread_loads(HALF);
-            __builtin_amdgcn_sched_barrier(0);
+        mfma(fa0, fb0, 0, 4);
 #pragma unroll
-            for (int h = 1; h + 1 < CH; ++h) chunk(buf, h);
-            __builtin_amdgcn_sched_barrier(0);
-            chunk(buf, CH - 1);
-            sstore(buf ^ 1);
-            spread_stores(FULL);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < NL; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
         }
-        __syncthreads();
-    }
+        __builtin_amdgcn_sched_barrier(0);
+        sstore(buf ^ 1);
+        mfma(fa1, fb1, 0, 3);
 #pragma unroll
-    for (int h = 0; h < CH; ++h) chunk((int)(st & 1), h);
+        for (int i = 0; i < NL; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        reads(buf ^ 1, 0, fa0, fb0);
+        mfma(fa1, fb1, 3, 4);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    reads((int)(st & 1), 1, fa1, fb1);
+    mfma(fa0, fb0, 0, 4);
+    mfma(fa1, fb1, 0, 4);
 
-    // D = alpha acc (+ beta C): acc[a][4 s + b][r] is row m0 + 64 wm + 16 a +
+    // D = alpha acc (+ beta C): acc[a][4 s + b][r] is row m0 + 128 wm + 16 a +
     // 4 lg + r, column n0 + 128 wn + 64 s + 4 c + b; a lane's four columns
     // are one 16-byte piece. Each row block's C pieces are loaded before its
     // stores (D may alias C).
@@ -193,8 +183,8 @@ void gemm_big_f32_kernel(GemmArgs g) {
     const float* C = static_cast<const float*>(g.C);
     const float alpha = (float)g.alpha, beta = (float)g.beta;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        const int64_t row0 = m0 + 64 * wm + 16 * a + 4 * lg;
+    for (int a = 0; a < 8; ++a) {
+        const int64_t row0 = m0 + 128 * wm + 16 * a + 4 * lg;
         f4_v cv[4][2];
         if (C) {
 #pragma unroll
@@ -221,22 +211,19 @@ void gemm_big_f32_kernel(GemmArgs g) {
 
 }  // namespace
 
-constexpr int kBigTM = 256, kBigBK = 32;
-
 // Whether gemm_big_f32 takes this problem (see the file comment).
 bool gemm_big_f32_fits(bool ta, bool tb, const GemmArgs& g) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    return !ta && !tb && g.batch == 1 && g.M % kBigTM == 0 && g.N % kBigN == 0 && g.K >= kBigBK &&
-           g.K % kBigBK == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.ldd % 4 == 0 && al(g.A) && al(g.B) &&
+    return !ta && !tb && g.batch == 1 && g.M % kBigM == 0 && g.N % kBigN == 0 && g.K >= kBigK &&
+           g.K % kBigK == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.ldd % 4 == 0 && al(g.A) && al(g.B) &&
            al(g.D) && (!g.C || (al(g.C) && g.ldc % 4 == 0));
 }
 
 int gemm_big_f32_launch(GemmArgs& g, hipStream_t st) {
-    g.tiles_m = g.M / kBigTM;
+    g.tiles_m = g.M / kBigM;
     g.tiles_n = g.N / kBigN;
     const int64_t tiles = g.tiles_m * g.tiles_n;
-    hipLaunchKernelGGL((gemm_big_f32_kernel<kBigTM, kBigBK>), dim3((unsigned)tiles),
-                       dim3(BigCfg<kBigTM, kBigBK>::T), 0, st, g);
+    hipLaunchKernelGGL(gemm_big_f32_kernel, dim3((unsigned)tiles), dim3(kBigThreads), 0, st, g);
     return check_launch("tt_gemm");
 }
 
