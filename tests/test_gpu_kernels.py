@@ -97,7 +97,8 @@ def test_gemm_batched_alpha_beta_ld(hip, dt, pad):
         (False, True, 2700, 2700, 40, 1),  # 128 x 128 tiles (484 of them), ragged edges
         (False, False, 200, 512, 48, 2),  # direct-B, 16-byte C pieces of two row blocks at a time, ragged M
         (True, False, 512, 768, 64, 3),  # direct-B, the batched shape family of config 2
-        (False, False, 4096, 4096, 96, 1),  # fp32: the 256 x 256 LDS tile, three stages
+        (False, False, 4096, 4096, 1024, 1),  # fp32: the 256 x 256 LDS tile (with C: K >= 1024)
+        (False, False, 512, 512, 1024, 64),  # fp32: the 256 x 256 LDS tile, batched, with C
     ],
 )
 def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
@@ -131,8 +132,10 @@ def test_gemm_d_aliases_c(hip, dt, ta, tb, M, N, K, batch):
         (False, 4160, 512, 48, 1, 1.5, 0.5, True, 0),
         (True, 4200, 768, 40, 2, 1.0, 0.0, False, 1),  # ragged last group and rows
         # fp32, whole 256 x 256 tiles, one per CU: the LDS-staged 256 x 256 tile kernel
-        (False, 4096, 4096, 64, 1, 1.5, 0.5, True, 0),
+        (False, 4096, 4096, 1024, 1, 1.5, 0.5, True, 0),
         (False, 2048, 8192, 32, 1, 1.0, 0.0, False, 0),  # one 32-k stage
+        (False, 512, 512, 512, 64, 1.0, 0.0, False, 0),  # batched, one tile per CU, no C
+        (False, 1024, 1024, 1024, 16, 1.5, 0.5, True, 0),  # batched with C, K >= 1024
     ],
 )
 def test_gemm_direct_b_matches_lds_tile(hip, dt, ta, M, N, K, batch, alpha, beta, with_c, ldd_pad):

@@ -1078,16 +1078,18 @@ static int gemm_typed(GemmArgs& g, bool ta, bool tb, hipStream_t st) {
     // against 0.1364 ms, 64 x 512^3 with alpha/beta and C 0.1397 against
     // 0.1414 ms, 4096^3 0.988 against 0.990 ms).
     // fp32, both operands not transposed, whole 256 x 256 tiles in whole
-    // rounds of one tile per CU (at least 95% of the last round busy): the
-    // 256 x 256 LDS tile (tt_gemm_big.hip), bitwise equal to the tiles
-    // below. Same box, alternating: 4096^3 with alpha/beta and C 0.968
-    // against 0.996 ms, without C 0.963 against 0.998; 8192^2 x 2048 1.930
-    // against 1.969; 2048 x 8192 x 4096 0.971 against 1.005 ms; 4096^2 x 1024
-    // 0.253 against 0.258 ms. A partial last round loses: 6144^2 x 2048 (2.25
-    // rounds) 1.444 against 1.118 ms, 5120^2 x 2048 0.961 against 0.869 ms.
+    // rounds of one tile per CU (at least 95% of the last round busy), without
+    // C or with K >= 1024: the 256 x 256 LDS tile (tt_gemm_big.hip), bitwise
+    // equal to the tiles below. Same box, alternating, fraction of the fp32
+    // peak against the 64 x 256 direct-B tile: 4096^3 with alpha/beta and C
+    // 0.93 against 0.88; 64 x 512^3 without C 0.834 against 0.806, 16 x
+    // 1024^3 with C 0.866 against 0.845. A partial last round loses (6144^2 x
+    // 2048, 2.25 rounds: 1.444 against 1.118 ms), and so does a short K with
+    // C, whose epilogue one wave per SIMD cannot hide (64 x 512^3 with C
+    // 0.785 against 0.801, 128 x 512^3 with C 0.760 against 0.799).
     if constexpr (sizeof(T) == 4 && !DOT)
-        if (gemm_big_f32_fits(ta, tb, g)) {
-            const int64_t tiles = (g.M / 256) * (g.N / 256), cus = device_cus();
+        if (gemm_big_f32_fits(ta, tb, g) && (!g.C || g.K >= 1024)) {
+            const int64_t tiles = (g.M / 256) * (g.N / 256) * g.batch, cus = device_cus();
             const int64_t rounds = (tiles + cus - 1) / cus;
             if (tiles >= cus && 100 * tiles >= 95 * rounds * cus) return gemm_big_f32_launch(g, st);
         }

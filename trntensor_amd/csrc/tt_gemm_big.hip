@@ -1,7 +1,7 @@
-// fp32 GEMM on 256 x 256 tiles with both operands staged through LDS
-// (tt_gemm, TT_F32, both operands not transposed, whole tiles, K a multiple
-// of 32, 16-byte aligned; the dispatcher takes it in whole rounds of one
-// tile per CU).
+// fp32 GEMM and batched GEMM on 256 x 256 tiles with both operands staged
+// through LDS (tt_gemm, TT_F32, both operands not transposed, whole tiles, K
+// a multiple of 32, 16-byte aligned; the dispatcher takes it in whole rounds
+// of one tile per CU, without C or with K >= 1024).
 //
 // Four waves of 128 x 128 (8 x 8 blocks of v_mfma_f32_16x16x4f32), one wave
 // per SIMD, one workgroup per CU (144 KiB of LDS). The 256 fp32 accumulators
@@ -58,17 +58,19 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_f32_kernel(GemmArgs g
     static_assert(NL == 16, "the schedule below spreads 16 loads, stores and fragment reads");
     __shared__ __attribute__((aligned(16))) float lds[2 * (AE + BE)];
 
-    // Rows of tiles in groups of four, each group column-major: an XCD's
-    // contiguous range of tiles is a block four tile rows high.
+    // Batch-major; within a product, rows of tiles in groups of four, each
+    // group column-major: an XCD's contiguous range of tiles is a block four
+    // tile rows high.
     const int64_t tiles = g.tiles_m * g.tiles_n;
-    const int64_t id = xcd_remap(blockIdx.x, tiles);
+    const int64_t id0 = xcd_remap(blockIdx.x, tiles * g.batch);
+    const int64_t bat = id0 / tiles, id = id0 - bat * tiles;
     const int64_t grp = id / (4 * g.tiles_n);
     const int64_t gm = min((int64_t)4, g.tiles_m - grp * 4);
     const int64_t rr = id - grp * 4 * g.tiles_n;
     const int64_t tn = rr / gm, tm = grp * 4 + rr % gm;
     const int64_t m0 = tm * kBigM, n0 = tn * kBigN;
-    const float* A = static_cast<const float*>(g.A);
-    const float* B = static_cast<const float*>(g.B);
+    const float* A = static_cast<const float*>(g.A) + bat * g.sA;
+    const float* B = static_cast<const float*>(g.B) + bat * g.sB;
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -177,22 +179,28 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_f32_kernel(GemmArgs g
 
     // D = alpha acc (+ beta C): acc[a][4 s + b][r] is row m0 + 128 wm + 16 a +
     // 4 lg + r, column n0 + 128 wn + 64 s + 4 c + b; a lane's four columns
-    // are one 16-byte piece. Each row block's C pieces are loaded before its
-    // stores (D may alias C).
-    float* D = static_cast<float*>(g.D);
-    const float* C = static_cast<const float*>(g.C);
+    // are one 16-byte piece.
+    float* D = static_cast<float*>(g.D) + bat * g.sD;
+    const float* C = g.C ? static_cast<const float*>(g.C) + bat * g.sC : nullptr;
     const float alpha = (float)g.alpha, beta = (float)g.beta;
+    // C of row blocks a and a + 1 in flight: block a + 2's loads are issued
+    // after block a's stores (they read other rows, so D may alias C).
+    f4_v cv[2][4][2];
+    auto cload = [&](int a, f4_v (&dst)[4][2]) __attribute__((always_inline)) {
+        const int64_t row0 = m0 + 128 * wm + 16 * a + 4 * lg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                dst[r][s] = *reinterpret_cast<const f4_v*>(C + (row0 + r) * g.ldc + n0 + 128 * wn + 64 * s + 4 * c);
+    };
+    if (C) {
+        cload(0, cv[0]);
+        cload(1, cv[1]);
+    }
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
         const int64_t row0 = m0 + 128 * wm + 16 * a + 4 * lg;
-        f4_v cv[4][2];
-        if (C) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    cv[r][s] = *reinterpret_cast<const f4_v*>(C + (row0 + r) * g.ldc + n0 + 128 * wn + 64 * s + 4 * c);
-        }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -202,10 +210,11 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_f32_kernel(GemmArgs g
                 for (int b = 0; b < 4; ++b) {
                     v[b] = acc[a][4 * s + b][r];
                     if (g.alpha != 1.0) v[b] = alpha * v[b];
-                    if (C) v[b] = v[b] + beta * cv[r][s][b];
+                    if (C) v[b] = v[b] + beta * cv[a & 1][r][s][b];
                 }
                 *reinterpret_cast<f4_v*>(D + (row0 + r) * g.ldd + n0 + 128 * wn + 64 * s + 4 * c) = v;
             }
+        if (C && a + 2 < 8) cload(a + 2, cv[a & 1]);
     }
 }
 
@@ -214,15 +223,17 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_big_f32_kernel(GemmArgs g
 // Whether gemm_big_f32 takes this problem (see the file comment).
 bool gemm_big_f32_fits(bool ta, bool tb, const GemmArgs& g) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    return !ta && !tb && g.batch == 1 && g.M % kBigM == 0 && g.N % kBigN == 0 && g.K >= kBigK &&
-           g.K % kBigK == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.ldd % 4 == 0 && al(g.A) && al(g.B) &&
-           al(g.D) && (!g.C || (al(g.C) && g.ldc % 4 == 0));
+    const bool batch_ok =
+        g.batch == 1 || (g.sA % 4 == 0 && g.sB % 4 == 0 && g.sD % 4 == 0 && (!g.C || g.sC % 4 == 0));
+    return !ta && !tb && batch_ok && g.M % kBigM == 0 && g.N % kBigN == 0 && g.K >= kBigK && g.K % kBigK == 0 &&
+           g.lda % 4 == 0 && g.ldb % 4 == 0 && g.ldd % 4 == 0 && al(g.A) && al(g.B) && al(g.D) &&
+           (!g.C || (al(g.C) && g.ldc % 4 == 0));
 }
 
 int gemm_big_f32_launch(GemmArgs& g, hipStream_t st) {
     g.tiles_m = g.M / kBigM;
     g.tiles_n = g.N / kBigN;
-    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t tiles = g.tiles_m * g.tiles_n * g.batch;
     hipLaunchKernelGGL(gemm_big_f32_kernel, dim3((unsigned)tiles), dim3(kBigThreads), 0, st, g);
     return check_launch("tt_gemm");
 }
