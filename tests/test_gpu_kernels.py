@@ -423,11 +423,14 @@ def test_mfma_rate_probe_closed_form(hip, code, dt, expected_per_iter, tol):
     (64, 3100, 16, 1, 1.5),            # one k-stage per tile
     (128, 3120, 48, 1, 1.0),           # two row tiles per column tile
     (192, 3120, 64, 8, -0.5),          # batched, three row tiles: tiles cross batch entries
+    (64, 3105, 64, 1, 1.0),            # N not a multiple of 256: fp64 keeps the 64 x 128 kernel
 ])
 def test_gemm_persistent_matches_per_tile_kernel(hip, dt, M, ntiles, K, batch, alpha):
     """A transposed, B row-major, no C, three or more rounds of 64-row tiles:
     the persistent direct-B kernel (each workgroup walks a list of tiles, the
-    next tile's first stage loaded during the current tile's last MFMAs).
+    next tile's first stage loaded during the current tile's last MFMAs), or
+    for fp64 with at most two row tiles and N a multiple of 256 its streaming
+    variant (64 x 256 tiles, two workgroups per CU).
     Bitwise equal to the per-tile direct-B kernel, which the same columns take
     in a launch of fewer tiles (the two keep one MFMA order per output), and
     checked against float64 torch on sampled columns."""

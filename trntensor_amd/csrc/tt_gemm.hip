@@ -922,6 +922,173 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
 }
 
+
+// Streaming direct-B GEMM (fp64, A transposed, B row-major, no C, at most two
+// 64-row tiles: the AO->MO half transform's shape, where B streams from HBM
+// once and feeds at most 128 rows). Persistent like
+// gemm_directb_persistent_kernel, but 64 x 256 tiles of four waves of 64 x 64
+// (NB = 4 column blocks), two workgroups per CU (two waves per SIMD), so
+// each A fragment read from LDS feeds 16 MFMAs instead of 8. Column block
+// 2 j + e of a lane is column 32 j + 2 c + e of its wave's 64: every 16-byte
+// B load and D store of a lane group covers 256 contiguous bytes. Per
+// 16-k stage: the next piece's A fragments are read ahead, the next stage's B
+// pieces are loaded one per 8 MFMAs, and the barrier comes before the last
+// piece, whose MFMAs cover the next stage's first fragment reads. The stages
+// of consecutive tiles form one pipeline (the next tile's first stage is
+// loaded during the current tile's last). MFMA order per output as
+// gemm_directb_kernel's: bitwise equal. Same box, alternating, against the
+// persistent 64 x 128 kernel: 64 x 786432 x 512 0.842-0.851 against
+// 0.880 ms, 64 x 393216 x 1024 0.819 against 0.855 ms, 128 x 393216 x 512
+// 0.775 against 0.803 ms; with five row tiles (the transform's batched
+// GEMM, 320 x 1536 x 512 x 64) it lost (0.490 against 0.483 ms), with 1.5
+// tiles per workgroup it tied. One wave per SIMD with NB = 8 (AGPR
+// accumulators) ran 0.951 ms.
+template <bool NT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_directb_stream_kernel(GemmArgs g) {
+    typedef Mfma<double> MF;
+    typedef typename MF::acc_t acc_t;
+    constexpr int NB = 4;
+    constexpr int BN = 64 * NB;
+    typedef typename Vec16<double>::type v16_t;
+    typedef Stage<double, 64, false, true, kBK> SA;
+    __shared__ __attribute__((aligned(16))) double lds[2 * SA::ELEMS];
+
+    // Hardware workgroup w runs on XCD w % 8; the tiles are split into eight
+    // contiguous ranges, one per XCD, taken round-robin by its workgroups.
+    const int64_t tiles = g.tiles_m * g.tiles_n;
+    const int64_t total = tiles * g.batch;
+    const int64_t x = blockIdx.x % kNumXcd;
+    const int64_t per = gridDim.x / kNumXcd;  // the grid is a multiple of 8
+    const int64_t hi = total * (x + 1) / kNumXcd;
+    int64_t id = total * x / kNumXcd + blockIdx.x / kNumXcd;
+    if (id >= hi) return;  // the whole workgroup: no barrier is left waiting
+    const int64_t nk = g.K / kBK;
+
+    const int lane = threadIdx.x & 63;
+    const int lg = lane >> 4;
+    const int c = lane & 15;
+    const int64_t wcol = (threadIdx.x >> 6) * (16 * NB) + 2 * c;
+    const int64_t boff = wcol + (int64_t)(4 * lg) * g.ldb;
+    struct Tile {
+        const double* A;
+        const double* B;
+        int64_t bat, tn, m0;
+    };
+    auto tile = [&](int64_t tid) __attribute__((always_inline)) -> Tile {
+        Tile u;
+        u.bat = tid / tiles;
+        const int64_t rem = tid - u.bat * tiles;
+        u.tn = rem / g.tiles_m;
+        u.m0 = (rem - u.tn * g.tiles_m) * 64;
+        u.A = static_cast<const double*>(g.A) + u.bat * g.sA;
+        u.B = static_cast<const double*>(g.B) + u.bat * g.sB + u.tn * BN;
+        return u;
+    };
+    SA sa;
+    v16_t rb[4][NB / 2];  // [piece p][j]: k-row 16 t + 4 lg + p, columns 32 j + 2 c, + 1
+    auto bload = [&](const double* B, int64_t t, int p) __attribute__((always_inline)) {
+        const double* q = B + (16 * t + p) * g.ldb + boff;
+#pragma unroll
+        for (int j = 0; j < NB / 2; ++j) {
+            const v16_t* qq = reinterpret_cast<const v16_t*>(q + 32 * j);
+            rb[p][j] = NT ? __builtin_nontemporal_load(qq) : *qq;
+        }
+    };
+    auto afrag = [&](const double* sbuf, int a, int s) __attribute__((always_inline)) -> double {
+        return sbuf[(4 * lg + s) * SA::PITCH + 16 * a + c];
+    };
+    acc_t acc[4][NB];
+    double fa[2][4];
+    auto piece = [&](int p, const double (&f)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[a][b] = MF::mma(f[a], rb[p][b >> 1][b & 1], acc[a][b]);
+    };
+    // Scheduling groups: the piece's A reads first (0x100), then one B load
+    // (0x020) after every 8 MFMAs (0x008).
+    auto spread = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < NB / 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One stage of the current tile from LDS buffer buf; stage tn1 of tile
+    // nxt is loaded behind it when `more`.
+    auto stage = [&](int buf, bool more, const Tile& nxt, int64_t tn1) __attribute__((always_inline)) {
+        if (more) sa.template load<true>(nxt.A, g.lda, nxt.m0, g.M, tn1 * kBK, g.K);
+        const double* sb = lds + buf * SA::ELEMS;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fa[(p + 1) & 1][a] = afrag(sb, a, p + 1);
+            piece(p, fa[p & 1]);
+            if (more) bload(nxt.B, tn1, p);
+            spread();
+        }
+        if (more) sa.store(lds + (buf ^ 1) * SA::ELEMS);
+        __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fa[0][a] = afrag(lds + (buf ^ 1) * SA::ELEMS, a, 0);
+        }
+        piece(3, fa[1]);
+        if (more) bload(nxt.B, tn1, 3);
+        spread();
+    };
+    auto store = [&](const Tile& u) __attribute__((always_inline)) {
+        double* D = static_cast<double*>(g.D) + u.bat * g.sD;
+        const int64_t col = u.tn * BN + wcol;
+        const double alpha = g.alpha;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = u.m0 + 16 * a + MF::row(lg, r);
+#pragma unroll
+                for (int j = 0; j < NB / 2; ++j) {
+                    v16_t v;
+                    v[0] = acc[a][2 * j][r];
+                    v[1] = acc[a][2 * j + 1][r];
+                    if (alpha != 1.0) v = v * alpha;
+                    *reinterpret_cast<v16_t*>(D + row * g.ldd + col + 32 * j) = v;
+                }
+            }
+    };
+
+    Tile cur = tile(id);
+    sa.template load<true>(cur.A, g.lda, cur.m0, g.M, 0, g.K);
+    sa.store(lds);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) bload(cur.B, 0, p);
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < 4; ++a) fa[0][a] = afrag(lds, a, 0);
+    int buf = 0;
+    for (;;) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[a][b] = acc_t{0, 0, 0, 0};
+        for (int64_t t = 0; t + 1 < nk; ++t) {
+            stage(buf, true, cur, t + 1);
+            buf ^= 1;
+        }
+        const int64_t nid = id + per;
+        const bool more = nid < hi;
+        const Tile nxt = tile(more ? nid : id);
+        stage(buf, more, nxt, 0);
+        buf ^= 1;
+        store(cur);
+        if (!more) break;
+        id = nid;
+        cur = nxt;
+    }
+}
+
 // Compute units of the current device (cached per device).
 static int device_cus() {
     static int cus[64];
@@ -953,6 +1120,20 @@ static int launch_directb(GemmArgs& g, bool ta, bool tb, bool nt, hipStream_t st
     const int64_t slots = (int64_t)device_cus() / kNumXcd * 4;
     const bool vecd = ((reinterpret_cast<uintptr_t>(g.D) | (uintptr_t)(g.ldd * sizeof(T)) |
                         (uintptr_t)(g.sD * sizeof(T))) & 15) == 0;
+    // fp64 with at most two row tiles and at least three 64 x 256 tiles per
+    // workgroup at two per CU: the streaming kernel.
+    if constexpr (sizeof(T) == 8 && !DOT) {
+        const int64_t stiles = g.tiles_m * (g.N / 256) * g.batch;
+        const int64_t sgrid = (int64_t)device_cus() / kNumXcd * kNumXcd * 2;
+        if (ta && !tb && full && !g.C && vecd && g.N % 256 == 0 && g.K >= kBK && g.K % kBK == 0 &&
+            g.tiles_m <= 2 && stiles >= 3 * sgrid) {
+            g.tiles_n = g.N / 256;
+            const dim3 grid((unsigned)sgrid), block(kThreads);
+            if (nt) hipLaunchKernelGGL((gemm_directb_stream_kernel<true>), grid, block, 0, st, g);
+            else hipLaunchKernelGGL((gemm_directb_stream_kernel<false>), grid, block, 0, st, g);
+            return check_launch("tt_gemm");
+        }
+    }
     if (!DOT && ta && !tb && full && !g.C && vecd && g.N % BN == 0 && g.K >= kBK && g.K % kBK == 0 &&
         total >= 3 * slots * kNumXcd) {
         const dim3 grid((unsigned)(slots * kNumXcd)), block(kThreads);
