@@ -470,7 +470,7 @@ def bench_c3(torch, tt, dev, args):
         "frac_mfma": round(flop / t / PEAK["f64"], 4),
         "frac_binding_roofline": round(t_floor / t, 4),
         "bound": "mfma (AI 14.2 flop/B > fp64 ridge 9.8)",
-        "kernel": "gemm_directb_persistent_kernel (A through LDS, B streamed into registers)",
+        "kernel": "gemm_directb_stream_kernel (A through LDS, B streamed into registers)",
     }
 
 
