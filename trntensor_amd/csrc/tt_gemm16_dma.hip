@@ -20,10 +20,12 @@
 // when every 16-lane quarter of a 16-byte access covers one 256-byte run
 // (BM = 128 moves half as many bytes again per MFMA).
 //
-// Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled so that each
-// 16-lane group of an MFMA operand read touches distinct banks):
+// Stage layouts in LDS (unpadded; 16-byte pieces XOR-swizzled against LDS
+// bank conflicts, the swizzles chosen by measurement):
 //   k-contiguous operand: row r (32 k = four pieces, 64 bytes) at r * 64,
-//     global piece p at position p ^ ((r >> 2) & 3);
+//     global piece p at position p ^ ((r >> 1) & 3) (bitwise-equal
+//     measurements, 4096^3 and 8192^3: +2.2-2.9% against (r >> 2) & 3;
+//     r & 3 and no swizzle no better);
 //   row-contiguous operand: k-row kr (ROWS rows = ROWS / 8 pieces, 2 ROWS
 //     bytes) at kr * 2 ROWS, global piece p at position p ^ (2 (kr & 3)).
 // Direct load q (0..ROWS/16 - 1) of an operand fills bytes [1024 q, 1024 q +
@@ -86,7 +88,7 @@ struct DStage {
         if (KC) {
             const int r = 16 * q + (lane >> 2);
             row = r;
-            k = 8 * ((lane & 3) ^ ((r >> 2) & 3));
+            k = 8 * ((lane & 3) ^ ((r >> 1) & 3));
         } else {
             const int kr = (1024 / KRB) * q + lane / (KRB / 16);
             k = kr;
@@ -113,7 +115,7 @@ struct DStage {
     __device__ __forceinline__ static du16x8 frag(const unsigned char* slot, int rb, int lane) {
         if (KC) {
             const int r = rb + (lane & 15), c = lane >> 4;
-            return *reinterpret_cast<const du16x8*>(slot + r * 64 + 16 * (c ^ ((r >> 2) & 3)));
+            return *reinterpret_cast<const du16x8*>(slot + r * 64 + 16 * (c ^ ((r >> 1) & 3)));
         }
         // Transposing reads: within 16 lanes, lane 4 j + a supplies the 8-byte
         // block of rows 4 b .. 4 b + 3 (b = rb / 4 + a) of k-row 8 g + 4 h + j,
