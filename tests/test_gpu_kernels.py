@@ -424,6 +424,7 @@ def test_mfma_rate_probe_closed_form(hip, code, dt, expected_per_iter, tol):
     (128, 3120, 48, 1, 1.0),           # two row tiles per column tile
     (192, 3120, 64, 8, -0.5),          # batched, three row tiles: tiles cross batch entries
     (64, 3105, 64, 1, 1.0),            # N not a multiple of 256: fp64 keeps the 64 x 128 kernel
+    (64, 3104, 32, 2, 2.0),            # fp64 streaming kernel, batched: tiles cross batch entries
 ])
 def test_gemm_persistent_matches_per_tile_kernel(hip, dt, M, ntiles, K, batch, alpha):
     """A transposed, B row-major, no C, three or more rounds of 64-row tiles:
@@ -490,4 +491,37 @@ def test_gemm_small_tile_matches_wide_tiles(hip, dt, M, N, K, batch, alpha, beta
         outs.append(D[:, :M])
     torch.cuda.synchronize()
     assert normwise(outs[0], ref) <= TOL[dt]
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("with_c", [False, True])
+def test_gemm_big_tile_broadcast_b(hip, with_c):
+    """fp32 batched products sharing one B (batch stride 0, the engine's
+    broadcast of an unbatched operand), whole 256 x 256 tiles filling the
+    chip: the 256 x 256 LDS tile (with C only for K >= 1024). Checked against
+    float64 torch, and bitwise against the LDS-staged tiles, which take the
+    same problem when B's leading dimension breaks 16-byte alignment."""
+    from trntensor_amd.hip import engine
+
+    dev = torch.device("cuda")
+    batch, M, N = 64, 512, 512
+    K = 1024 if with_c else 512
+    g = torch.Generator().manual_seed(K + batch)
+    A = torch.randn(batch, M, K, generator=g, dtype=torch.float64)
+    B = torch.randn(K, N + 1, generator=g, dtype=torch.float64)
+    C = torch.randn(batch, M, N, generator=g, dtype=torch.float64)
+    ref = 1.5 * torch.matmul(A, B[:, :N])
+    if with_c:
+        ref = ref + 0.5 * C
+    Ad, Cd = A.to(dev, torch.float32), C.to(dev, torch.float32)
+    Bn = B[:, :N].contiguous().to(dev, torch.float32)  # ldb = N: the 256 x 256 tile
+    Bo = B.contiguous().to(dev, torch.float32)  # ldb = N + 1: the LDS-staged tiles
+    outs = []
+    for Bd, ldb in ((Bn, N), (Bo, N + 1)):
+        D = torch.full((batch, M, N), float("nan"), dtype=torch.float32, device=dev)
+        engine.gemm(False, False, M, N, K, Ad, K, M * K, Bd, ldb, 0, D, N, M * N, batch, 1.5, 0.5,
+                    Cd if with_c else None, N, M * N)
+        outs.append(D)
+    torch.cuda.synchronize()
+    assert normwise(outs[0].cpu().double(), ref) <= TOL[torch.float32]
     assert torch.equal(outs[0], outs[1])
