@@ -1039,6 +1039,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_directb_stream_kernel(GemmAr
         if (more) bload(nxt.B, tn1, 3);
         spread();
     };
+    // D is written once and not read here: non-temporal stores (64 x 786432
+    // x 512, same box, alternating, three runs: 0.838-0.845 against
+    // 0.844-0.849 ms; K 1024 with N / 2: 0.818 against 0.813 ms).
     auto store = [&](const Tile& u) __attribute__((always_inline)) {
         double* D = static_cast<double*>(g.D) + u.bat * g.sD;
         const int64_t col = u.tn * BN + wcol;
@@ -1054,7 +1057,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_directb_stream_kernel(GemmAr
                     v[0] = acc[a][2 * j][r];
                     v[1] = acc[a][2 * j + 1][r];
                     if (alpha != 1.0) v = v * alpha;
-                    *reinterpret_cast<v16_t*>(D + row * g.ldd + col + 32 * j) = v;
+                    __builtin_nontemporal_store(v, reinterpret_cast<v16_t*>(D + row * g.ldd + col + 32 * j));
                 }
             }
     };
