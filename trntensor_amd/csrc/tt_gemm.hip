@@ -942,7 +942,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 // 0.775 against 0.803 ms; with five row tiles (the transform's batched
 // GEMM, 320 x 1536 x 512 x 64) it lost (0.490 against 0.483 ms), with 1.5
 // tiles per workgroup it tied. One wave per SIMD with NB = 8 (AGPR
-// accumulators) ran 0.951 ms.
+// accumulators) ran 0.951 against 0.914 ms on another box, and B two stages
+// ahead (238 VGPRs) 0.907 against 0.852 ms.
 template <bool NT>
 __global__ __launch_bounds__(kThreads, 2) void gemm_directb_stream_kernel(GemmArgs g) {
     typedef Mfma<double> MF;
